@@ -1,0 +1,327 @@
+"""ctypes binding of the CPU oracle (oracle/vx_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the parity checker and the CPU baseline.  Only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this.
+The product never does.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "libvx_oracle.so")
+
+
+def build(force=False):
+    """Compile the oracle with its Makefile (gcc)."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+class Config(ctypes.Structure):
+    _fields_ = [
+        ("dim", ctypes.c_int), ("n_layers", ctypes.c_int),
+        ("head_dim", ctypes.c_int), ("hidden_dim", ctypes.c_int),
+        ("n_heads", ctypes.c_int), ("n_kv_heads", ctypes.c_int),
+        ("vocab_size", ctypes.c_int), ("rope_theta", ctypes.c_float),
+        ("norm_eps", ctypes.c_float), ("fm_layers", ctypes.c_int),
+        ("nfe", ctypes.c_int), ("cfg_alpha", ctypes.c_float),
+        ("n_acoustic_out", ctypes.c_int), ("semantic_vocab", ctypes.c_int),
+        ("acoustic_levels", ctypes.c_int), ("audio_vocab", ctypes.c_int),
+    ]
+
+
+_lib = None
+P = np.ctypeslib.ndpointer
+F32 = P(dtype=np.float32, flags="C_CONTIGUOUS")
+U16 = P(dtype=np.uint16, flags="C_CONTIGUOUS")
+U32 = P(dtype=np.uint32, flags="C_CONTIGUOUS")
+c_int, c_float, c_u64, c_size = ctypes.c_int, ctypes.c_float, ctypes.c_uint64, ctypes.c_size_t
+c_vp = ctypes.c_void_p
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        build()
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "vxo_default_config": (None, [ctypes.POINTER(Config)]),
+            "vxo_f32_to_f16": (ctypes.c_uint16, [c_float]),
+            "vxo_f16_to_f32": (c_float, [ctypes.c_uint16]),
+            "vxo_splitmix64_next": (c_u64, [ctypes.POINTER(c_u64)]),
+            "vxo_name_stream": (c_u64, [ctypes.c_char_p]),
+            "vxo_normal": (c_float, [c_u64, c_u64, c_u64]),
+            "vxo_gen_f32": (None, [c_u64, c_u64, c_size, c_float, c_float, F32]),
+            "vxo_gen_f16": (None, [c_u64, c_u64, c_size, c_float, c_float, U16]),
+            "vxo_matvec_f16": (None, [U16, F32, F32, c_int, c_int]),
+            "vxo_rmsnorm": (None, [F32, U16, F32, c_int, c_float]),
+            "vxo_embedding": (None, [U16, c_int, c_int, F32]),
+            "vxo_rope": (None, [F32, c_int, c_int, c_int, c_float]),
+            "vxo_attn_scores": (None, [F32, F32, F32, c_int, c_int, c_int, c_int]),
+            "vxo_softmax": (None, [F32, c_int, c_int]),
+            "vxo_attn_value": (None, [F32, F32, F32, c_int, c_int, c_int, c_int]),
+            "vxo_swiglu": (None, [F32, F32, c_int]),
+            "vxo_time_embedding": (None, [F32, c_int, c_float]),
+            "vxo_cfg_combine": (None, [F32, F32, c_int, c_float]),
+            "vxo_euler_step": (None, [F32, F32, c_int, c_float]),
+            "vxo_fsq_quantize": (None, [F32, U32, c_int, c_int, c_int]),
+            "vxo_argmax": (ctypes.c_uint32, [F32, c_int]),
+            "vxo_multi_codebook_embed": (None, [U16, ctypes.c_uint32, U32, c_int, F32]),
+            "vxo_bi_attention": (None, [F32, F32, F32, F32, F32, c_int, c_int, c_int, c_int]),
+            "vxo_create": (c_vp, [ctypes.POINTER(Config), c_int]),
+            "vxo_destroy": (None, [c_vp]),
+            "vxo_set_weight": (c_int, [c_vp, ctypes.c_char_p, U16]),
+            "vxo_init_synthetic": (c_int, [c_vp, c_u64, c_float]),
+            "vxo_weight_numel": (c_size, [c_vp, ctypes.c_char_p]),
+            "vxo_weight": (c_vp, [c_vp, ctypes.c_char_p]),
+            "vxo_is_ready": (c_int, [c_vp]),
+            "vxo_reset": (None, [c_vp]),
+            "vxo_position": (c_int, [c_vp]),
+            "vxo_set_position": (None, [c_vp, c_int]),
+            "vxo_buffer": (c_vp, [c_vp, ctypes.c_char_p, ctypes.POINTER(c_int)]),
+            "vxo_kv": (c_vp, [c_vp, c_int, c_int]),
+            "vxo_acoustic_codes": (c_vp, [c_vp]),
+            "vxo_semantic_argmax": (ctypes.c_uint32, [c_vp]),
+            "vxo_set_semantic_code": (None, [c_vp, ctypes.c_uint32]),
+            "vxo_set_acoustic_codes": (None, [c_vp, U32]),
+            "vxo_argmax_result": (ctypes.c_uint32, [c_vp]),
+            "vxo_backbone_step": (None, [c_vp, c_int, c_int, c_vp, c_int]),
+            "vxo_backbone_step_ex": (None, [c_vp, c_int, c_int, c_vp, c_int, c_vp]),
+            "vxo_backbone_step_codes": (None, [c_vp]),
+            "vxo_fm_forward": (None, [c_vp, F32]),
+            "vxo_fm_forward_batched": (None, [c_vp, F32]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def default_config(**over):
+    c = Config()
+    lib().vxo_default_config(ctypes.byref(c))
+    for k, v in over.items():
+        setattr(c, k, v)
+    return c
+
+
+# ---------------------------------------------------------------- numbers
+def name_stream(name):
+    return lib().vxo_name_stream(name.encode())
+
+
+def gen_f32(seed, name, n, mean=0.0, std=1.0):
+    out = np.empty(n, np.float32)
+    lib().vxo_gen_f32(seed, name_stream(name), n, mean, std, out)
+    return out
+
+
+def gen_f16(seed, name, n, mean=0.0, std=1.0):
+    out = np.empty(n, np.uint16)
+    lib().vxo_gen_f16(seed, name_stream(name), n, mean, std, out)
+    return out
+
+
+def f16_bits_to_f32(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+# ---------------------------------------------------------------- kernels
+def matvec_f16(A_bits, x):
+    M, K = A_bits.shape
+    y = np.empty(M, np.float32)
+    lib().vxo_matvec_f16(np.ascontiguousarray(A_bits), np.ascontiguousarray(x, np.float32), y, M, K)
+    return y
+
+
+def rmsnorm(x, w_bits, eps=1e-5):
+    y = np.empty_like(x, dtype=np.float32)
+    lib().vxo_rmsnorm(np.ascontiguousarray(x, np.float32), np.ascontiguousarray(w_bits), y, x.size, eps)
+    return y
+
+
+def rope(qk, head_dim, pos, theta):
+    out = np.ascontiguousarray(qk, np.float32).copy()
+    lib().vxo_rope(out, head_dim, pos, out.size // head_dim, theta)
+    return out
+
+
+def attention_decode(q, kcache, vcache, n_heads, n_kv_heads, head_dim, seq_len):
+    """attnScore + softmax + attnValue; caches are [seq][n_kv*hd] f32."""
+    scores = np.empty(n_heads * seq_len, np.float32)
+    out = np.empty(n_heads * head_dim, np.float32)
+    L = lib()
+    kc = np.ascontiguousarray(kcache, np.float32)
+    vc = np.ascontiguousarray(vcache, np.float32)
+    L.vxo_attn_scores(np.ascontiguousarray(q, np.float32), kc, scores, n_heads, n_kv_heads, head_dim, seq_len)
+    L.vxo_softmax(scores, n_heads, seq_len)
+    L.vxo_attn_value(scores, vc, out, n_heads, n_kv_heads, head_dim, seq_len)
+    return out, scores
+
+
+def swiglu(g, u):
+    out = np.ascontiguousarray(g, np.float32).copy()
+    lib().vxo_swiglu(out, np.ascontiguousarray(u, np.float32), out.size)
+    return out
+
+
+def time_embedding(dim, t):
+    out = np.empty(dim, np.float32)
+    lib().vxo_time_embedding(out, dim, t)
+    return out
+
+
+def cfg_combine(vc, vu, alpha):
+    out = np.ascontiguousarray(vc, np.float32).copy()
+    lib().vxo_cfg_combine(out, np.ascontiguousarray(vu, np.float32), out.size, alpha)
+    return out
+
+
+def euler_step(x, v, dt):
+    out = np.ascontiguousarray(x, np.float32).copy()
+    lib().vxo_euler_step(out, np.ascontiguousarray(v, np.float32), out.size, dt)
+    return out
+
+
+def fsq_quantize(x, levels=21, offset=2):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.size, np.uint32)
+    lib().vxo_fsq_quantize(x, out, x.size, levels, offset)
+    return out
+
+
+def argmax(x):
+    return int(lib().vxo_argmax(np.ascontiguousarray(x, np.float32), x.size))
+
+
+def multi_codebook_embed(table_bits, semantic_code, acoustic_codes, dim):
+    out = np.empty(dim, np.float32)
+    lib().vxo_multi_codebook_embed(np.ascontiguousarray(table_bits), semantic_code,
+                                   np.ascontiguousarray(acoustic_codes, np.uint32), dim, out)
+    return out
+
+
+def bi_attention(q, k, v, n_heads, n_kv_heads, head_dim, seq_len=3):
+    scores = np.empty(n_heads * seq_len * seq_len, np.float32)
+    out = np.empty(seq_len * n_heads * head_dim, np.float32)
+    lib().vxo_bi_attention(np.ascontiguousarray(q, np.float32), np.ascontiguousarray(k, np.float32),
+                           np.ascontiguousarray(v, np.float32), scores, out,
+                           n_heads, n_kv_heads, head_dim, seq_len)
+    return out, scores
+
+
+# ---------------------------------------------------------------- engine
+class OracleEngine:
+    """CPU restatement of VoxtralEngine's device state (src/engine.ts)."""
+
+    def __init__(self, cfg=None, max_seq=4096):
+        self.cfg = cfg if cfg is not None else default_config()
+        self.max_seq = max_seq
+        self._h = lib().vxo_create(ctypes.byref(self.cfg), max_seq)
+        self._keep = {}
+
+    def close(self):
+        if self._h:
+            lib().vxo_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def init_synthetic(self, seed=0, std=0.02):
+        if lib().vxo_init_synthetic(self._h, seed, std) != 0:
+            raise MemoryError("oracle synthetic weights")
+
+    def set_weight(self, name, bits):
+        bits = np.ascontiguousarray(bits, np.uint16).ravel()
+        if bits.size != lib().vxo_weight_numel(self._h, name.encode()):
+            raise ValueError(f"bad size for {name}")
+        self._keep[name] = bits
+        if lib().vxo_set_weight(self._h, name.encode(), bits) != 0:
+            raise KeyError(name)
+
+    def weight(self, name):
+        n = lib().vxo_weight_numel(self._h, name.encode())
+        p = lib().vxo_weight(self._h, name.encode())
+        if not n or not p:
+            raise KeyError(name)
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint16)), (n,))
+
+    @property
+    def is_ready(self):
+        return bool(lib().vxo_is_ready(self._h))
+
+    @property
+    def position(self):
+        return lib().vxo_position(self._h)
+
+    @position.setter
+    def position(self, p):
+        lib().vxo_set_position(self._h, p)
+
+    def reset(self):
+        lib().vxo_reset(self._h)
+
+    def buffer(self, name):
+        n = c_int(0)
+        p = lib().vxo_buffer(self._h, name.encode(), ctypes.byref(n))
+        if not p:
+            raise KeyError(name)
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), (n.value,))
+
+    def kv(self, layer, which):
+        p = lib().vxo_kv(self._h, layer, which)
+        kvd = self.cfg.n_kv_heads * self.cfg.head_dim
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), (self.max_seq, kvd))
+
+    @property
+    def acoustic_codes(self):
+        p = lib().vxo_acoustic_codes(self._h)
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint32)),
+                                     (self.cfg.n_acoustic_out,)).copy()
+
+    @acoustic_codes.setter
+    def acoustic_codes(self, codes):
+        lib().vxo_set_acoustic_codes(self._h, np.ascontiguousarray(codes, np.uint32))
+
+    @property
+    def semantic_code(self):
+        return int(lib().vxo_semantic_argmax(self._h))
+
+    @semantic_code.setter
+    def semantic_code(self, c):
+        lib().vxo_set_semantic_code(self._h, int(c))
+
+    @property
+    def argmax_result(self):
+        return int(lib().vxo_argmax_result(self._h))
+
+    def backbone_step(self, token=0, mode=0, precomputed=None, lm_head=False, layer_out=False):
+        pre = None
+        if precomputed is not None:
+            pre = np.ascontiguousarray(precomputed, np.float32)
+            mode = 2
+        lo = None
+        if layer_out:
+            lo = np.empty((self.cfg.n_layers, 2, self.cfg.dim), np.float32)
+        lib().vxo_backbone_step_ex(self._h, int(token), int(mode),
+                                   pre.ctypes.data if pre is not None else None,
+                                   int(bool(lm_head)),
+                                   lo.ctypes.data if lo is not None else None)
+        return lo
+
+    def backbone_step_codes(self):
+        lib().vxo_backbone_step_codes(self._h)
+
+    def fm_forward(self, noise, batched=False):
+        noise = np.ascontiguousarray(noise, np.float32)
+        (lib().vxo_fm_forward_batched if batched else lib().vxo_fm_forward)(self._h, noise)
