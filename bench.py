@@ -1,0 +1,169 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Voxtral frame loop (one JSON line on stdout).
+
+Workload (the headline configuration): the full 26-layer backbone
+(dim 3072, 32/8 heads of 128, FFN 9216, random-init f16 weights N(0,0.02)),
+batch 1, decoding at context 512 after a real prefill of a seeded random
+512-token prefix (ids uniform over 131072).  A step is one complete decode
+step (26 layers + final norm; the LM head is off, as in generate()), with
+all inputs resident in HBM.  value = decode steps (frames) per second.
+
+Also reported: the full frame loop (backbone step + 3-layer flow-matching
+CFG Euler loop, greedy semantic code on the device, 500 frames from
+context 512) as x-real-time (one frame = 80 ms of audio), the roofline of
+the dominant kernel, and the CPU oracle timed on the host cores.
+Diagnostics go to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "webgpu-voxtral_amd"))
+
+METRIC = "backbone decode frames/s @ctx512 + % HBM roofline, full frame loop x-realtime"
+HBM_PEAK_GBPS = 8000.0
+CTX = 512
+LAYERS = 26
+# algorithmic HBM bytes (f16 weights, f16 KV)
+LAYER_WEIGHT_BYTES = 232_796_160          # q,k,v,o,w1,w2,w3 + 2 norms
+KV_BYTES_PER_KEY = 26 * 2 * 1024 * 2      # K and V rows of every layer
+FM_EULER_BYTES = 698_836_992              # 3 FM layers + input/acoustic proj + norm
+FM_FRAME_BYTES = 69_992_448               # semantic head + llm projection
+EMB_CODES_BYTES = 37 * 3072 * 2           # 37-row multi-codebook sum
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def step_bytes(keys):
+    return LAYERS * LAYER_WEIGHT_BYTES + KV_BYTES_PER_KEY * keys + KV_BYTES_PER_KEY
+
+
+def cpu_baseline(target_s):
+    """The oracle (C restatement of the reference kernels, OpenMP) on the
+    host: full-depth 26-layer decode steps at context 512, no LM head."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle as O
+    from vxtest import fill_oracle_kv
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    t0 = time.time()
+    o = O.OracleEngine(O.default_config(), max_seq=CTX + 1)
+    o.init_synthetic(0, 0.02)
+    fill_oracle_kv(o, 0, CTX)
+    log(f"[cpu] oracle ready in {time.time() - t0:.1f}s ({threads} threads)")
+    x = O.gen_f32(0, "input.hidden", 3072)
+    times = []
+    while sum(times) < target_s and len(times) < 50:
+        o.position = CTX
+        t = time.perf_counter()
+        o.backbone_step(precomputed=x)
+        times.append(time.perf_counter() - t)
+    med = float(np.median(times[1:] if len(times) > 2 else times))
+    o.close()
+    return {"value": 1.0 / med, "unit": "frames/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} full 26-layer decode steps at context 512 (median of "
+                      f"{max(1, len(times) - 1)} after 1 warm-up), C oracle restating the "
+                      f"reference WGSL kernels, OpenMP {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--frames", type=int, default=500)
+    ap.add_argument("--kernel-iters", type=int, default=104)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-frames", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the frame loop runs on a single MI355X "
+              "(multi-GPU sharding is a design note, not a measured path); use --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import voxtral_amd as V
+    t0 = time.time()
+    eng = V.VoxtralEngine(V.default_config(), max_seq_len=4096).init()
+    eng.init_synthetic(0, 0.02)
+    toks = np.random.default_rng(0).integers(0, 131072, CTX)
+    for t in toks:
+        eng.backbone_step(int(t), read_normed=False)
+    assert eng.position == CTX
+    log(f"[gpu] weights + {CTX}-token prefill in {time.time() - t0:.1f}s")
+
+    # ---- headline: decode steps at context 512 (513 keys each)
+    eng.time_backbone_steps(args.warmup, hold_position=True)
+    ms = eng.time_backbone_steps(args.steps, hold_position=True)
+    ms_step = ms / args.steps
+    value = 1000.0 / ms_step
+    sb = step_bytes(CTX + 1)
+    step_gbps = sb / (ms_step * 1e-3) / 1e9
+    log(f"[gpu] decode {ms_step * 1000:.1f} us/step -> {value:.1f} frames/s, "
+        f"{step_gbps:.0f} GB/s ({step_gbps / HBM_PEAK_GBPS:.1%} of peak)")
+
+    # ---- dominant kernel: gate/up GEMV (+RMSNorm prologue, SwiGLU epilogue)
+    kern = {}
+    for k, name in enumerate(V.KERNEL_NAMES):
+        us, b = eng.time_kernel(k, args.kernel_iters)
+        kern[name] = {"avg_us": us, "bytes": b, "GBps": b / (us * 1e-6) / 1e9}
+        log(f"[gpu] kernel {name:7s} {us:8.2f} us  {b / 1e6:8.2f} MB  {kern[name]['GBps']:7.0f} GB/s")
+    dom = kern["gateup"]
+    roofline = {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": "gemv_kernel<gate/up + RMSNorm + SwiGLU>", "launch_bytes": dom["bytes"],
+                "avg_us": round(dom["avg_us"], 3)}
+
+    # ---- full frame loop (backbone + FM CFG Euler loop), 500 frames
+    frame = None
+    if not args.no_frames:
+        eng.position = CTX
+        eng.debug_write("normed", np.zeros(3072, np.float32))
+        eng.fm_step_and_read()  # seeds the device codes read by the first frame
+        eng.time_frames(5)
+        eng.position = CTX
+        fms = eng.time_frames(args.frames)
+        fps = args.frames * 1000.0 / fms
+        keys_avg = CTX + 1 + (args.frames - 1) / 2.0
+        fb = step_bytes(keys_avg) + 7 * FM_EULER_BYTES + FM_FRAME_BYTES + EMB_CODES_BYTES
+        frame = {"frames": args.frames, "ms_per_frame": round(fms / args.frames, 4),
+                 "frames_per_s": round(fps, 2), "x_realtime": round(fps * 0.08, 2),
+                 "bytes_per_frame": fb,
+                 "hbm_frac": round(fb * fps / 1e9 / HBM_PEAK_GBPS, 4),
+                 "sampling": "greedy masked argmax on device, no EOS"}
+        log(f"[gpu] frame loop {fms / args.frames * 1000:.1f} us/frame -> {fps:.1f} frames/s "
+            f"= {fps * 0.08:.1f}x real-time")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"[cpu] {cpu['value']:.3f} frames/s on {cpu['cores']} threads")
+    eng.destroy()
+
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "frames/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 weights, f32 accumulate", "data": "synthetic",
+        "config": {"workload": "26-layer backbone decode, batch 1, context 512 (513 keys), "
+                               "after a real 512-token prefill", "layers": LAYERS,
+                   "context": CTX, "batch": 1, "parallelism": "none (1 GPU)"},
+        "step_hbm": {"bytes": sb, "achieved_GBps": round(step_gbps, 1),
+                     "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
+        "roofline": roofline, "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()}
+                                          for k, v in kern.items()},
+        "frame_loop": frame, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,226 @@
+/*
+ * voxtral_engine.h -- C ABI of the MI355X Voxtral frame-loop engine
+ * (libvoxtral_amd.so).
+ *
+ * The library replaces the WebGPU engine of svenflow/webgpu-voxtral
+ * (src/engine.ts, class VoxtralEngine) for the per-frame token loop: the
+ * 26-layer backbone decode step and the flow-matching CFG Euler loop.  Every
+ * entry point below names the reference method it stands in for.  Plain C
+ * types only: host arrays are copied in and out; the engine owns all device
+ * memory.
+ *
+ * Conventions
+ *   - Every function returning int returns VX_OK (0) or a negative VX_E*
+ *     code; vx_last_error() then holds the message (per handle; a NULL
+ *     handle reads the message of the last failed vx_create).
+ *   - A handle is not thread safe: one caller at a time.  All work of a
+ *     handle runs in order on one HIP stream that the handle owns.
+ *   - Weights are IEEE binary16 bit patterns, row-major [out, in], exactly
+ *     the tensors the reference loads (src/engine.ts:659-743).
+ */
+#ifndef VOXTRAL_ENGINE_H
+#define VOXTRAL_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VX_OK 0
+#define VX_E_INVALID -1    /* bad argument, shape or name */
+#define VX_E_STATE -2      /* e.g. called before all weights are loaded */
+#define VX_E_DEVICE -3     /* HIP runtime error */
+#define VX_E_RANGE -4      /* position would pass max_seq_len */
+#define VX_E_NOMEM -5
+
+typedef struct vx_engine vx_engine;
+
+/* Model constants, src/types.ts:70-122 (backbone + fm + the codec constant
+ * the FSQ step reads).  The HIP kernels are specialised for the default
+ * values; vx_create rejects other shapes. */
+typedef struct vx_config {
+  int32_t dim;             /* 3072 */
+  int32_t n_layers;        /* 26 (1..26 accepted: single-layer workloads) */
+  int32_t head_dim;        /* 128 */
+  int32_t hidden_dim;      /* 9216 */
+  int32_t n_heads;         /* 32 */
+  int32_t n_kv_heads;      /* 8 */
+  int32_t vocab_size;      /* 131072 */
+  float rope_theta;        /* 1e6 */
+  float norm_eps;          /* 1e-5 */
+  int32_t fm_layers;       /* 3 */
+  int32_t nfe;             /* 8 timesteps -> nfe-1 Euler updates */
+  float cfg_alpha;         /* 1.2 */
+  int32_t n_acoustic_out;  /* 36 */
+  int32_t semantic_vocab;  /* 8320 */
+  int32_t acoustic_levels; /* 21 */
+  int32_t audio_vocab;     /* 9088 */
+} vx_config;
+
+/* defaultConfig, src/types.ts:70-122 */
+int vx_config_default(vx_config *cfg);
+
+/* new VoxtralEngine({config, maxSeqLen}) + init(), src/engine.ts:301-340.
+ * max_seq_len: KV slots per layer (reference default 4096). */
+int vx_create(const vx_config *cfg, int32_t max_seq_len, vx_engine **out);
+
+/* destroy(), src/engine.ts:2621-2632 */
+void vx_destroy(vx_engine *e);
+
+const char *vx_last_error(const vx_engine *e);
+
+/* One tensor of loadWeights()/loadWeightsFromHF() + organizeWeights(),
+ * src/engine.ts:539-586, 659-743.  `name` is the reference tensor name, e.g.
+ * "layers.3.attention.wq.weight"; `shape` must match.  Unknown names are
+ * VX_E_INVALID ("Missing weight" is reported by vx_is_ready()). */
+int vx_load_tensor(vx_engine *e, const char *name, const uint16_t *f16,
+                   size_t numel, const int64_t *shape, int32_t ndim);
+
+/* No counterpart in the reference: fills every weight on the device from
+ * the counter-based generator (seed, tensor name), mean 0 and std `std`
+ * (norm gains: mean 1).  For synthetic benchmarks; bit-identical to the
+ * CPU oracle's generator. */
+int vx_init_synthetic(vx_engine *e, uint64_t seed, float std);
+
+/* isReady getter, src/engine.ts:2047-2049.  1 when every weight is loaded. */
+int vx_is_ready(const vx_engine *e);
+
+/* reset(), src/engine.ts:2323-2327: position = 0 (stale KV is never read). */
+int vx_reset(vx_engine *e);
+int32_t vx_position(const vx_engine *e);
+int vx_set_position(vx_engine *e, int32_t pos);
+
+/* Embedding source of a backbone step (src/engine.ts:814-854). */
+#define VX_EMBED_TOKEN 0       /* row `token` of tok_embeddings */
+#define VX_EMBED_AUDIO 1       /* row `token` of audio_codebook_embeddings */
+#define VX_EMBED_PRECOMPUTED 2 /* `precomputed` f32[dim] replaces it */
+#define VX_EMBED_CODES 3       /* multi-codebook sum of the device codes */
+
+/* backboneStep + position++ (src/engine.ts:814-1042; public forms
+ * backboneStepAndRead :2333-2342 and debugBackboneStepFull :2348-2357).
+ * lm_head != 0 also runs the tied LM head and its argmax (written to
+ * *argmax_out when not NULL).  normed_out (nullable) receives the final-norm
+ * output f32[dim] (W.normed). */
+int vx_backbone_step(vx_engine *e, int32_t token, int32_t embed_mode,
+                     const float *precomputed, int32_t lm_head,
+                     uint32_t *argmax_out, float *normed_out);
+
+/* debugBackboneLayerByLayer read points, src/engine.ts:2106-2287: one step
+ * that also copies the hidden state after each attention residual and each
+ * FFN residual into layer_out[n_layers][2][dim]. */
+int vx_backbone_step_layers(vx_engine *e, int32_t token, int32_t embed_mode,
+                            const float *precomputed, float *layer_out);
+
+/* fmForward (src/engine.ts:1240-1380; public form debugFMStep :2363-2380).
+ * noise: f32[36] (debugNoise) or NULL for the engine's seeded generator.
+ * Outputs (each nullable): semantic logits f32[8320], acoustic codes
+ * u32[36], final x_t f32[36].  The unmasked tree argmax of the logits is
+ * stored as the device semantic code (W.semantic_argmax). */
+int vx_fm_forward(vx_engine *e, const float *noise, float *semantic_logits,
+                  uint32_t *acoustic_codes, float *x_final);
+
+/* writeBuffer(W.semantic_argmax), src/engine.ts:2574-2575, and the
+ * teacher-forcing counterpart for the acoustic codes. */
+int vx_set_semantic_code(vx_engine *e, uint32_t code);
+int vx_set_acoustic_codes(vx_engine *e, const uint32_t *codes36);
+int vx_get_codes(vx_engine *e, uint32_t *semantic, uint32_t *codes36);
+
+/* debugRead(name, count), src/engine.ts:2062-2067.  Names: hidden, normed,
+ * q, attn_out, gate (SwiGLU output), logits, semantic_logits, x_t,
+ * velocity, v_uncond, fm_hidden (llm projection), fm_seq (6 x dim: cond
+ * positions 0..2 then uncond), time_proj (table of nfe-1 rows). */
+int vx_read(vx_engine *e, const char *buffer, float *dst, size_t count);
+
+/* queue.writeBuffer into a work buffer (the reference's only host->device
+ * activation path, e.g. src/engine.ts:1266-1274, 2574-2575); names:
+ * "hidden" (next step input is not affected: steps embed first), "normed"
+ * (input of the next vx_fm_forward -- teacher forcing). */
+int vx_write(vx_engine *e, const char *buffer, const float *src, size_t count);
+
+/* KV cache access (no reference counterpart; test and prefill plumbing).
+ * Layout seen by the caller: [pos][n_kv_heads * head_dim] f16 bits, the
+ * reference's [maxSeq, 1024] row order (src/engine.ts:510-530). */
+int vx_write_kv(vx_engine *e, int32_t layer, int32_t which /*0=K,1=V*/,
+                int32_t pos0, int32_t npos, const uint16_t *f16);
+int vx_read_kv(vx_engine *e, int32_t layer, int32_t which, int32_t pos0,
+               int32_t npos, uint16_t *f16);
+/* Fills positions [0, npos) of every layer's K and V with N(0,1) f16 from
+ * the generator (stream "kv.<layer>.k"/"kv.<layer>.v", element index
+ * pos*1024 + c). */
+int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos);
+
+/* ----------------------------------------------------------- generate() */
+#define VX_SAMPLE_TOP_P 0  /* reference: masked top-p 0.9, T 0.8 on host */
+#define VX_SAMPLE_GREEDY 1 /* masked argmax on the device, no readback */
+
+typedef struct vx_generate_options {
+  int32_t sampling;   /* VX_SAMPLE_* */
+  float top_p;        /* 0.9 */
+  float temperature;  /* 0.8 */
+  uint64_t seed;      /* noise + sampling seed (reference: Math.random) */
+  int32_t ignore_eos; /* 1: run exactly max_frames (benchmarks) */
+} vx_generate_options;
+
+typedef struct vx_generate_stats {
+  double backbone_ms; /* prefill (TTSResult.stats.backboneMs) */
+  double fm_ms;       /* frame loop (stats.fmMs) */
+  double codec_ms;    /* 0: the codec decoder is not part of this library */
+  double total_ms;
+  int32_t frames_generated;
+} vx_generate_stats;
+
+/* onFrame(frame, semanticCode, acousticCodes) and onStage(stage, doneMs)
+ * of generate(), src/engine.ts:2416-2424.  stage: 0 backbone, 1 fm,
+ * 2 codec; done_ms < 0 marks a stage start. */
+typedef void (*vx_frame_cb)(void *user, int32_t frame, uint32_t semantic,
+                            const uint32_t *acoustic36);
+typedef void (*vx_stage_cb)(void *user, int32_t stage, double done_ms);
+
+void vx_generate_options_default(vx_generate_options *o);
+
+/* generate(tokens, audioTokenStart, audioTokenCount, voiceEmbeddings,
+ * maxFrames, onFrame, onStage), src/engine.ts:2416-2616, without the codec
+ * decode.  voice: f32[audio_count][dim] or NULL.  semantic_out[max_frames]
+ * and acoustic_out[max_frames][36] receive the codes (nullable). */
+int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens,
+                int32_t audio_start, int32_t audio_count, const float *voice,
+                int32_t max_frames, const vx_generate_options *opt,
+                vx_frame_cb on_frame, vx_stage_cb on_stage, void *user,
+                uint32_t *semantic_out, uint32_t *acoustic_out,
+                vx_generate_stats *stats);
+
+/* ------------------------------------------------------ measurement */
+/* No reference counterparts (the reference times on the CPU,
+ * src/benchmark.ts:277-320).  Each runs on the handle's stream, bracketed
+ * by HIP events, inputs resident in HBM. */
+
+/* n backbone decode steps (graph replays), each starting from the hidden
+ * state the previous step left; LM head off.  *ms = total event time.
+ * hold_position = 0: positions advance by n (the context grows);
+ * hold_position != 0: every step decodes at the current position (reads
+ * the same number of keys, rewrites that KV row) and position stays. */
+int vx_time_backbone_steps(vx_engine *e, int32_t n, int32_t hold_position,
+                           float *ms);
+/* n frames of the full loop (multi-codebook embed + backbone + FM, greedy
+ * codes on the device, no EOS), as one graph replay each. */
+int vx_time_frames(vx_engine *e, int32_t n, float *ms);
+
+#define VX_KERNEL_QKV 0
+#define VX_KERNEL_ATTN 1
+#define VX_KERNEL_OPROJ 2
+#define VX_KERNEL_GATEUP 3
+#define VX_KERNEL_DOWN 4
+/* Average duration of one launch of a backbone kernel (cycling over the
+ * layers so no launch finds its weights in cache); *bytes = algorithmic
+ * HBM bytes of one launch at the current position. */
+int vx_time_kernel(vx_engine *e, int32_t kernel, int32_t iters, float *avg_us,
+                   double *bytes);
+
+int vx_synchronize(vx_engine *e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

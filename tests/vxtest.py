@@ -1,0 +1,59 @@
+"""Shared helpers of the parity tests: the comparison functions and engine
+pairs (HIP engine + CPU oracle) built from the same seeded synthetic data."""
+import numpy as np
+
+import oracle as O
+
+SEED = 0
+STD = 0.02
+
+
+def max_rel_err(actual, expected):
+    """max |a-e| / max(|e|, 1e-2*||e||_inf): the hidden-state tolerance
+    metric (bound 1e-2 for f16 weights with f32 accumulation)."""
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    floor = 1e-2 * max(np.abs(e).max(), 1e-30)
+    return float(np.max(np.abs(a - e) / np.maximum(np.abs(e), floor)))
+
+
+def ref_allclose(actual, expected, atol=0.01, rtol=0.01):
+    """allclose of the reference test utilities (src/npy.ts:122-169):
+    passes when |a-e| <= atol + rtol*|e| everywhere."""
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    return bool(np.all(np.abs(a - e) <= atol + rtol * np.abs(e)))
+
+
+def oracle_engine(n_layers=1, fm_layers=3, max_seq=1024, seed=SEED, std=STD):
+    cfg = O.default_config(n_layers=n_layers, fm_layers=fm_layers)
+    e = O.OracleEngine(cfg, max_seq=max_seq)
+    e.init_synthetic(seed, std)
+    return e
+
+
+def gpu_engine(n_layers=1, fm_layers=3, max_seq=1024, seed=SEED, std=STD):
+    import voxtral_amd as V
+    cfg = V.default_config(n_layers=n_layers, fm_layers=fm_layers)
+    g = V.VoxtralEngine(cfg, max_seq_len=max_seq).init()
+    g.init_synthetic(seed, std)
+    return g
+
+
+def fill_oracle_kv(o, seed, npos):
+    """Same synthetic KV rows as vx_fill_kv_synthetic: f16 N(0,1) from the
+    generator stream kv.<layer>.k / .v, held as f32 by the oracle."""
+    kvd = o.cfg.n_kv_heads * o.cfg.head_dim
+    for l in range(o.cfg.n_layers):
+        for w, nm in ((0, "k"), (1, "v")):
+            bits = O.gen_f16(seed, f"kv.{l}.{nm}", npos * kvd)
+            o.kv(l, w)[:npos] = O.f16_bits_to_f32(bits).reshape(npos, kvd)
+
+
+def masked_tree_argmax(logits):
+    """Greedy semantic code: index 0 and >= 8194 masked (src/engine.ts:
+    2556-2563), then the 256-lane tree argmax."""
+    x = np.array(logits, np.float32, copy=True)
+    x[0] = -np.inf
+    x[8194:] = -np.inf
+    return O.argmax(x)

@@ -1,0 +1,1022 @@
+// vx_engine.hip -- host side of libvoxtral_amd.so: the C ABI declared in
+// include/voxtral_engine.h.  Replaces the WebGPU dispatch layer and
+// orchestration of src/engine.ts (backboneStep :814-1042, fmForward
+// :1240-1380, generate :2416-2616) with HIP launches on one stream, the
+// per-step kernel sequence captured once into hipGraphs.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/voxtral_engine.h"
+#include "vx_kernels.h"
+
+using namespace vx;
+
+namespace {
+
+char g_create_error[512] = "";
+
+struct LayerW {
+  uint16_t *wqkv = nullptr, *wo = nullptr, *w1 = nullptr, *w3 = nullptr, *w2 = nullptr,
+           *attn_norm = nullptr, *ffn_norm = nullptr;
+};
+
+struct Slot {
+  uint16_t *ptr;
+  std::vector<int64_t> shape;
+  size_t numel;
+  bool is_norm;
+  bool loaded;
+};
+
+// FNV-1a 64 of "fm.noise": generator stream of the per-frame FM noise
+constexpr uint64_t kNoiseStream = 0x45237962ac6f43f0ull;
+
+constexpr size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+}  // namespace
+
+struct vx_engine {
+  vx_config cfg;
+  int max_seq = 0;
+  hipStream_t st = nullptr;
+  std::string err;
+
+  // weights
+  void *warena = nullptr;
+  std::vector<LayerW> L, FL;
+  uint16_t *tok_emb = nullptr, *audio_emb = nullptr, *final_norm = nullptr;
+  uint16_t *fm_in = nullptr, *fm_llm = nullptr, *fm_time = nullptr, *fm_norm = nullptr,
+           *fm_sem = nullptr, *fm_ac = nullptr;
+  std::map<std::string, Slot> slots;
+
+  // KV cache [layer][K|V][NKV][max_seq][HD]
+  uint16_t *kv = nullptr;
+
+  // activations
+  void *aarena = nullptr;
+  float *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *normed = nullptr,
+        *logits = nullptr, *part = nullptr, *layer_stage = nullptr;
+  int *counter = nullptr, *pos = nullptr, *frame = nullptr;
+  uint32_t *sem_code = nullptr, *codes = nullptr, *argmax_res = nullptr;
+  uint64_t *noise_seed = nullptr;
+  float *fm_seq = nullptr, *fm_q = nullptr, *fm_k = nullptr, *fm_v = nullptr, *fm_attn = nullptr,
+        *fm_act = nullptr, *fm_llm_out = nullptr, *sem_logits = nullptr, *tproj = nullptr,
+        *xh = nullptr, *vel = nullptr, *noise = nullptr, *time_embed = nullptr;
+  bool tproj_ready = false;
+
+  int host_pos = 0;
+  hipGraphExec_t step_exec = nullptr, hold_exec = nullptr, frame_exec = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+
+  uint16_t *kc(int l) const { return kv + (size_t)(2 * l) * NKV * max_seq * HD; }
+  uint16_t *vc(int l) const { return kv + (size_t)(2 * l + 1) * NKV * max_seq * HD; }
+  int nsteps() const { return cfg.nfe - 1; }
+};
+
+// ----------------------------------------------------------------- errors
+static int fail(vx_engine *e, int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (e)
+    e->err = buf;
+  else
+    snprintf(g_create_error, sizeof g_create_error, "%s", buf);
+  return code;
+}
+
+#define HIPCHK(e, call)                                                            \
+  do {                                                                             \
+    hipError_t _s = (call);                                                        \
+    if (_s != hipSuccess)                                                          \
+      return fail((e), VX_E_DEVICE, "%s failed: %s", #call, hipGetErrorString(_s)); \
+  } while (0)
+
+#define LAUNCHCHK(e)                                                                  \
+  do {                                                                                \
+    hipError_t _s = hipGetLastError();                                                \
+    if (_s != hipSuccess)                                                             \
+      return fail((e), VX_E_DEVICE, "kernel launch failed: %s", hipGetErrorString(_s)); \
+  } while (0)
+
+static uint64_t fnv1a(const char *s) {
+  uint64_t h = 0xcbf29ce484222325ull;
+  for (; *s; s++) {
+    h ^= (unsigned char)*s;
+    h *= 0x100000001b3ull;
+  }
+  return h;
+}
+
+// ------------------------------------------------------- kernel launchers
+namespace {
+
+// Launch shapes.  Rows per block = WAVES * RPW (SwiGLU: pairs = WAVES*RPW/2).
+constexpr int W4 = 4;
+
+template <int NB, int WAVES, int RPW, int EPI, bool NORM, int K, int KT>
+void launch_gemv(hipStream_t st, const GemvArgs &a) {
+  constexpr int units = WAVES * (EPI == EPI_SWIGLU ? RPW / 2 : RPW);
+  const int grid = (a.M + units - 1) / units;
+  hipLaunchKernelGGL((gemv_kernel<NB, WAVES, RPW, EPI, NORM, K, KT>), dim3(grid),
+                     dim3(WAVES * 64), 0, st, a);
+}
+
+GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, int M) {
+  GemvArgs a;
+  memset(&a, 0, sizeof a);
+  a.W = W;
+  a.x = x;
+  a.xs = xs;
+  a.out = out;
+  a.os = os;
+  a.M = M;
+  return a;
+}
+
+}  // namespace
+
+// One backbone layer: 5 launches (QKV+rope+KV write | attention | O +
+// residual | norm + gate/up + SwiGLU | down + residual).
+static void enqueue_layer(vx_engine *e, int l, int only = -1) {
+  const LayerW &W = e->L[l];
+  hipStream_t st = e->st;
+  if (only < 0 || only == VX_KERNEL_QKV) {
+    GemvArgs a = gargs(W.wqkv, e->x, DIM, e->q, 0, QKV_ROWS);
+    a.norm_w = W.attn_norm;
+    a.eps = e->cfg.norm_eps;
+    a.pos = e->pos;
+    a.kc = e->kc(l);
+    a.vc = e->vc(l);
+    a.max_seq = e->max_seq;
+    a.theta = e->cfg.rope_theta;
+    launch_gemv<1, W4, 2, EPI_QKV_ROPE, true, DIM, DIM>(st, a);
+  }
+  if (only < 0 || only == VX_KERNEL_ATTN) {
+    AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->counter, e->attn};
+    hipLaunchKernelGGL(attn_decode_kernel, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
+  }
+  if (only < 0 || only == VX_KERNEL_OPROJ) {
+    GemvArgs a = gargs(W.wo, e->attn, QD, e->x, 0, DIM);
+    launch_gemv<1, W4, 1, EPI_RESID, false, QD, QD>(st, a);
+  }
+  if (only < 0 || only == VX_KERNEL_GATEUP) {
+    GemvArgs a = gargs(W.w1, e->x, DIM, e->act, 0, HID);
+    a.W2 = W.w3;
+    a.norm_w = W.ffn_norm;
+    a.eps = e->cfg.norm_eps;
+    launch_gemv<1, W4, 2, EPI_SWIGLU, true, DIM, DIM>(st, a);
+  }
+  if (only < 0 || only == VX_KERNEL_DOWN) {
+    GemvArgs a = gargs(W.w2, e->act, HID, e->x, 0, DIM);
+    launch_gemv<1, W4, 1, EPI_RESID, false, HID, HID>(st, a);
+  }
+}
+
+static void enqueue_backbone_at(vx_engine *e, bool advance) {
+  for (int l = 0; l < e->cfg.n_layers; l++) enqueue_layer(e, l);
+  hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->final_norm,
+                     e->cfg.norm_eps, e->normed, advance ? e->pos : nullptr);
+}
+static void enqueue_backbone(vx_engine *e) { enqueue_backbone_at(e, true); }
+static void enqueue_backbone_hold(vx_engine *e) { enqueue_backbone_at(e, false); }
+
+static void enqueue_lm_head(vx_engine *e) {
+  GemvArgs a = gargs(e->tok_emb, e->normed, DIM, e->logits, 0, e->cfg.vocab_size);
+  launch_gemv<1, W4, 2, EPI_PLAIN, false, DIM, DIM>(e->st, a);
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, e->st, e->logits, e->cfg.vocab_size, 0,
+                     e->argmax_res);
+}
+
+static int ensure_tproj(vx_engine *e) {
+  if (e->tproj_ready) return VX_OK;
+  for (int s = 0; s < e->nsteps(); s++) {
+    float t = (float)((double)s / (double)(e->cfg.nfe - 1));
+    hipLaunchKernelGGL(time_embed_kernel, dim3((DIM / 2 + 255) / 256), dim3(256), 0, e->st,
+                       e->time_embed, t);
+    GemvArgs a = gargs(e->fm_time, e->time_embed, DIM, e->tproj + (size_t)s * DIM, 0, DIM);
+    launch_gemv<1, W4, 2, EPI_PLAIN, false, DIM, DIM>(e->st, a);
+  }
+  LAUNCHCHK(e);
+  e->tproj_ready = true;
+  return VX_OK;
+}
+
+// fmForward with CFG batched: 6 vectors (2 branches x 3 positions) share
+// every weight read; time projections come from the precomputed table.
+// noise_src: device f32[36] holding x_0.
+static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
+  hipStream_t st = e->st;
+  const float alpha = e->cfg.cfg_alpha;
+  const float dt = (float)(1.0 / (double)(e->cfg.nfe - 1));
+  {
+    GemvArgs a = gargs(e->fm_sem, e->normed, DIM, e->sem_logits, 0, SEMV);
+    launch_gemv<1, W4, 2, EPI_PLAIN, false, DIM, DIM>(st, a);
+    GemvArgs b = gargs(e->fm_llm, e->normed, DIM, e->fm_llm_out, 0, DIM);
+    launch_gemv<1, W4, 2, EPI_PLAIN, false, DIM, DIM>(st, b);
+    // unmasked tree argmax (W.semantic_argmax), or masked for greedy codes
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, st, e->sem_logits, SEMV,
+                       greedy_code ? 8194 : 0, e->sem_code);
+  }
+  for (int s = 0; s < e->nsteps(); s++) {
+    FmStepArgs fa{e->xh, e->vel, e->fm_in, e->tproj + (size_t)s * DIM, e->fm_llm_out, e->fm_seq,
+                  s, alpha, dt, noise_src};
+    hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256), dim3(256), 0, st, fa);
+    for (int l = 0; l < e->cfg.fm_layers; l++) {
+      const LayerW &W = e->FL[l];
+      {
+        GemvArgs a = gargs(W.wqkv, e->fm_seq, DIM, e->fm_q, 0, QKV_ROWS);
+        a.out_k = e->fm_k;
+        a.out_v = e->fm_v;
+        a.norm_w = W.attn_norm;
+        a.eps = 1e-5f;
+        launch_gemv<6, W4, 2, EPI_QKV, true, DIM, 1536>(st, a);
+      }
+      hipLaunchKernelGGL(fm_attn_kernel, dim3(NH, 2), dim3(64), 0, st, e->fm_q, e->fm_k, e->fm_v,
+                         e->fm_attn);
+      {
+        GemvArgs a = gargs(W.wo, e->fm_attn, QD, e->fm_seq, DIM, DIM);
+        launch_gemv<6, W4, 1, EPI_RESID, false, QD, 1024>(st, a);
+      }
+      {
+        GemvArgs a = gargs(W.w1, e->fm_seq, DIM, e->fm_act, HID, HID);
+        a.W2 = W.w3;
+        a.norm_w = W.ffn_norm;
+        a.eps = 1e-5f;
+        launch_gemv<6, W4, 2, EPI_SWIGLU, true, DIM, 1536>(st, a);
+      }
+      {
+        GemvArgs a = gargs(W.w2, e->fm_act, HID, e->fm_seq, DIM, DIM);
+        launch_gemv<6, W4, 1, EPI_RESID, false, HID, 1536>(st, a);
+      }
+    }
+    {  // final norm of position 0 of each branch -> acoustic_out -> vel[s]
+      GemvArgs a = gargs(e->fm_ac, e->fm_seq, 3 * DIM, e->vel + (size_t)s * 2 * NAC, NAC, NAC);
+      a.norm_w = e->fm_norm;
+      a.eps = 1e-5f;
+      launch_gemv<2, W4, 1, EPI_PLAIN, true, DIM, DIM>(st, a);
+    }
+  }
+  hipLaunchKernelGGL(fm_finish_kernel, dim3(1), dim3(64), 0, st, e->xh, e->vel, e->nsteps() - 1,
+                     alpha, dt, e->codes, e->cfg.acoustic_levels, e->frame);
+}
+
+// ------------------------------------------------------------------ graphs
+static int capture(vx_engine *e, hipGraphExec_t *out, void (*body)(vx_engine *)) {
+  hipGraph_t g;
+  HIPCHK(e, hipStreamBeginCapture(e->st, hipStreamCaptureModeThreadLocal));
+  body(e);
+  hipError_t cap = hipStreamEndCapture(e->st, &g);
+  if (cap != hipSuccess) return fail(e, VX_E_DEVICE, "graph capture: %s", hipGetErrorString(cap));
+  hipError_t s = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (s != hipSuccess) return fail(e, VX_E_DEVICE, "graph instantiate: %s", hipGetErrorString(s));
+  return VX_OK;
+}
+
+static void frame_body(vx_engine *e) {
+  hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
+                     e->sem_code, e->codes, e->x);
+  enqueue_backbone(e);
+  hipLaunchKernelGGL(fm_noise_kernel, dim3(1), dim3(64), 0, e->st, e->noise, e->noise_seed,
+                     kNoiseStream, e->frame);
+  enqueue_fm(e, e->noise, true);
+}
+
+static int ensure_graphs(vx_engine *e) {
+  if (!e->step_exec) {
+    int rc = capture(e, &e->step_exec, enqueue_backbone);
+    if (rc) return rc;
+  }
+  return VX_OK;
+}
+
+// ---------------------------------------------------------------- helpers
+__global__ void set_int_kernel(int *p, int v) { *p = v; }
+__global__ void set_u32_kernel(uint32_t *p, const uint32_t v0) { *p = v0; }
+
+static int check_ready(vx_engine *e) {
+  for (auto &kv : e->slots)
+    if (!kv.second.loaded) return fail(e, VX_E_STATE, "Missing weight: %s", kv.first.c_str());
+  return VX_OK;
+}
+
+static int prepare_input(vx_engine *e, int32_t token, int32_t mode, const float *pre) {
+  if (e->host_pos >= e->max_seq)
+    return fail(e, VX_E_RANGE, "position %d reaches max_seq_len %d", e->host_pos, e->max_seq);
+  switch (mode) {
+    case VX_EMBED_TOKEN:
+      if (token < 0 || token >= e->cfg.vocab_size)
+        return fail(e, VX_E_INVALID, "token %d outside vocab", token);
+      hipLaunchKernelGGL(embed_row_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->tok_emb, token,
+                         e->x);
+      break;
+    case VX_EMBED_AUDIO:
+      if (token < 0 || token >= e->cfg.audio_vocab)
+        return fail(e, VX_E_INVALID, "audio token %d outside table", token);
+      hipLaunchKernelGGL(embed_row_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
+                         token, e->x);
+      break;
+    case VX_EMBED_PRECOMPUTED:
+      if (!pre) return fail(e, VX_E_INVALID, "precomputed embedding is NULL");
+      HIPCHK(e, hipMemcpyAsync(e->x, pre, DIM * sizeof(float), hipMemcpyHostToDevice, e->st));
+      break;
+    case VX_EMBED_CODES:
+      hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
+                         e->sem_code, e->codes, e->x);
+      break;
+    default:
+      return fail(e, VX_E_INVALID, "bad embed mode %d", mode);
+  }
+  LAUNCHCHK(e);
+  return VX_OK;
+}
+
+// ================================================================ C ABI
+extern "C" {
+
+int vx_config_default(vx_config *c) {
+  if (!c) return VX_E_INVALID;
+  c->dim = 3072;
+  c->n_layers = 26;
+  c->head_dim = 128;
+  c->hidden_dim = 9216;
+  c->n_heads = 32;
+  c->n_kv_heads = 8;
+  c->vocab_size = 131072;
+  c->rope_theta = 1000000.0f;
+  c->norm_eps = 1e-5f;
+  c->fm_layers = 3;
+  c->nfe = 8;
+  c->cfg_alpha = 1.2f;
+  c->n_acoustic_out = 36;
+  c->semantic_vocab = 8320;
+  c->acoustic_levels = 21;
+  c->audio_vocab = 9088;
+  return VX_OK;
+}
+
+const char *vx_last_error(const vx_engine *e) { return e ? e->err.c_str() : g_create_error; }
+
+static void add_slot(vx_engine *e, const std::string &name, uint16_t *ptr,
+                     std::vector<int64_t> shape, bool is_norm) {
+  size_t n = 1;
+  for (auto s : shape) n *= (size_t)s;
+  e->slots[name] = Slot{ptr, shape, n, is_norm, false};
+}
+
+int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
+  if (!out) return fail(nullptr, VX_E_INVALID, "out is NULL");
+  *out = nullptr;
+  vx_config cfg;
+  vx_config_default(&cfg);
+  if (cfg_in) cfg = *cfg_in;
+  if (cfg.dim != DIM || cfg.head_dim != HD || cfg.n_heads != NH || cfg.n_kv_heads != NKV ||
+      cfg.hidden_dim != HID || cfg.n_acoustic_out != NAC || cfg.semantic_vocab != SEMV)
+    return fail(nullptr, VX_E_INVALID,
+                "unsupported shape: the kernels are built for dim 3072, 32/8 heads of 128, "
+                "FFN 9216, 36 acoustic dims, semantic vocab 8320");
+  if (cfg.n_layers < 1 || cfg.n_layers > 64 || cfg.fm_layers < 1 || cfg.fm_layers > 16 ||
+      cfg.nfe < 2 || cfg.nfe > 64 || cfg.vocab_size < 25 || cfg.audio_vocab < 9022 ||
+      cfg.acoustic_levels < 2)
+    return fail(nullptr, VX_E_INVALID, "config out of range");
+  if (max_seq < 1 || max_seq > (1 << 20))
+    return fail(nullptr, VX_E_INVALID, "max_seq_len %d out of range", max_seq);
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1)
+    return fail(nullptr, VX_E_DEVICE, "No HIP device");
+
+  vx_engine *e = new vx_engine();
+  e->cfg = cfg;
+  e->max_seq = max_seq;
+  if (hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking) != hipSuccess) {
+    delete e;
+    return fail(nullptr, VX_E_DEVICE, "hipStreamCreate failed");
+  }
+  (void)hipEventCreate(&e->ev0);
+  (void)hipEventCreate(&e->ev1);
+
+  // ---- weight table (names: src/engine.ts:659-743)
+  struct Req {
+    std::string name;
+    std::vector<int64_t> shape;
+    bool norm;
+    uint16_t **dst;
+    size_t off_rows;  // for q/k/v inside the stacked QKV matrix
+  };
+  const int nl = cfg.n_layers, fl = cfg.fm_layers;
+  e->L.resize(nl);
+  e->FL.resize(fl);
+  size_t total = 0;
+  auto reserve = [&](size_t elems) {
+    size_t o = total;
+    total += align256(elems * 2);
+    return o;
+  };
+  // offsets first, pointers after the arena exists
+  struct Off {
+    uint16_t **dst;
+    size_t off;
+  };
+  std::vector<Off> offs;
+  auto place = [&](uint16_t **dst, size_t elems) { offs.push_back({dst, reserve(elems)}); };
+  place(&e->tok_emb, (size_t)cfg.vocab_size * DIM);
+  place(&e->audio_emb, (size_t)cfg.audio_vocab * DIM);
+  place(&e->final_norm, DIM);
+  auto place_layer = [&](LayerW &W) {
+    place(&W.wqkv, (size_t)QKV_ROWS * DIM);
+    place(&W.wo, (size_t)DIM * QD);
+    place(&W.w1, (size_t)HID * DIM);
+    place(&W.w3, (size_t)HID * DIM);
+    place(&W.w2, (size_t)DIM * HID);
+    place(&W.attn_norm, DIM);
+    place(&W.ffn_norm, DIM);
+  };
+  for (auto &W : e->L) place_layer(W);
+  for (auto &W : e->FL) place_layer(W);
+  place(&e->fm_in, (size_t)DIM * NAC);
+  place(&e->fm_llm, (size_t)DIM * DIM);
+  place(&e->fm_time, (size_t)DIM * DIM);
+  place(&e->fm_norm, DIM);
+  place(&e->fm_sem, (size_t)SEMV * DIM);
+  place(&e->fm_ac, (size_t)NAC * DIM);
+  if (hipMalloc(&e->warena, total) != hipSuccess) {
+    vx_destroy(e);
+    return fail(nullptr, VX_E_NOMEM, "hipMalloc of %zu weight bytes failed", total);
+  }
+  for (auto &o : offs) *o.dst = (uint16_t *)((char *)e->warena + o.off);
+
+  add_slot(e, "mm_audio_embeddings.tok_embeddings.weight", e->tok_emb, {cfg.vocab_size, DIM}, false);
+  add_slot(e, "mm_audio_embeddings.audio_codebook_embeddings.embeddings.weight", e->audio_emb,
+           {cfg.audio_vocab, DIM}, false);
+  add_slot(e, "norm.weight", e->final_norm, {DIM}, true);
+  auto layer_slots = [&](const std::string &p, LayerW &W) {
+    add_slot(e, p + ".attention_norm.weight", W.attn_norm, {DIM}, true);
+    add_slot(e, p + ".attention.wq.weight", W.wqkv, {QD, DIM}, false);
+    add_slot(e, p + ".attention.wk.weight", W.wqkv + (size_t)QD * DIM, {KVD, DIM}, false);
+    add_slot(e, p + ".attention.wv.weight", W.wqkv + (size_t)(QD + KVD) * DIM, {KVD, DIM}, false);
+    add_slot(e, p + ".attention.wo.weight", W.wo, {DIM, QD}, false);
+    add_slot(e, p + ".ffn_norm.weight", W.ffn_norm, {DIM}, true);
+    add_slot(e, p + ".feed_forward.w1.weight", W.w1, {HID, DIM}, false);
+    add_slot(e, p + ".feed_forward.w2.weight", W.w2, {DIM, HID}, false);
+    add_slot(e, p + ".feed_forward.w3.weight", W.w3, {HID, DIM}, false);
+  };
+  for (int i = 0; i < nl; i++) layer_slots("layers." + std::to_string(i), e->L[i]);
+  for (int i = 0; i < fl; i++)
+    layer_slots("acoustic_transformer.layers." + std::to_string(i), e->FL[i]);
+  add_slot(e, "acoustic_transformer.input_projection.weight", e->fm_in, {DIM, NAC}, false);
+  add_slot(e, "acoustic_transformer.llm_projection.weight", e->fm_llm, {DIM, DIM}, false);
+  add_slot(e, "acoustic_transformer.time_projection.weight", e->fm_time, {DIM, DIM}, false);
+  add_slot(e, "acoustic_transformer.norm.weight", e->fm_norm, {DIM}, true);
+  add_slot(e, "acoustic_transformer.semantic_codebook_output.weight", e->fm_sem, {SEMV, DIM}, false);
+  add_slot(e, "acoustic_transformer.acoustic_codebook_output.weight", e->fm_ac, {NAC, DIM}, false);
+
+  // ---- KV cache
+  size_t kvbytes = (size_t)nl * 2 * NKV * max_seq * HD * 2;
+  if (hipMalloc(&e->kv, kvbytes) != hipSuccess) {
+    vx_destroy(e);
+    return fail(nullptr, VX_E_NOMEM, "hipMalloc of %zu KV bytes failed", kvbytes);
+  }
+  (void)hipMemsetAsync(e->kv, 0, kvbytes, e->st);
+
+  // ---- activations
+  size_t abytes = 0;
+  std::vector<std::pair<void **, size_t>> aoffs;
+  auto aplace = [&](void **dst, size_t bytes) {
+    aoffs.push_back({dst, abytes});
+    abytes += align256(bytes);
+  };
+  const int ns = cfg.nfe - 1;
+  aplace((void **)&e->x, DIM * 4);
+  aplace((void **)&e->q, QD * 4);
+  aplace((void **)&e->attn, QD * 4);
+  aplace((void **)&e->act, HID * 4);
+  aplace((void **)&e->normed, DIM * 4);
+  aplace((void **)&e->logits, (size_t)cfg.vocab_size * 4);
+  aplace((void **)&e->part, (size_t)NH * ATTN_SPLITS * (HD + 2) * 4);
+  aplace((void **)&e->layer_stage, (size_t)nl * 2 * DIM * 4);
+  aplace((void **)&e->counter, 64 * 4);
+  aplace((void **)&e->pos, 4);
+  aplace((void **)&e->frame, 4);
+  aplace((void **)&e->sem_code, 4);
+  aplace((void **)&e->codes, 64 * 4);
+  aplace((void **)&e->argmax_res, 4);
+  aplace((void **)&e->noise_seed, 8);
+  aplace((void **)&e->fm_seq, 6 * DIM * 4);
+  aplace((void **)&e->fm_q, 6 * QD * 4);
+  aplace((void **)&e->fm_k, 6 * KVD * 4);
+  aplace((void **)&e->fm_v, 6 * KVD * 4);
+  aplace((void **)&e->fm_attn, 6 * QD * 4);
+  aplace((void **)&e->fm_act, 6 * HID * 4);
+  aplace((void **)&e->fm_llm_out, DIM * 4);
+  aplace((void **)&e->sem_logits, SEMV * 4);
+  aplace((void **)&e->tproj, (size_t)ns * DIM * 4);
+  aplace((void **)&e->xh, (size_t)(ns + 1) * NAC * 4);
+  aplace((void **)&e->vel, (size_t)ns * 2 * NAC * 4);
+  aplace((void **)&e->noise, NAC * 4);
+  aplace((void **)&e->time_embed, DIM * 4);
+  if (hipMalloc(&e->aarena, abytes) != hipSuccess) {
+    vx_destroy(e);
+    return fail(nullptr, VX_E_NOMEM, "hipMalloc of activations failed");
+  }
+  for (auto &o : aoffs) *o.first = (char *)e->aarena + o.second;
+  (void)hipMemsetAsync(e->aarena, 0, abytes, e->st);
+  if (hipStreamSynchronize(e->st) != hipSuccess) {
+    vx_destroy(e);
+    return fail(nullptr, VX_E_DEVICE, "device initialisation failed");
+  }
+  *out = e;
+  return VX_OK;
+}
+
+void vx_destroy(vx_engine *e) {
+  if (!e) return;
+  if (e->st) (void)hipStreamSynchronize(e->st);
+  if (e->step_exec) (void)hipGraphExecDestroy(e->step_exec);
+  if (e->hold_exec) (void)hipGraphExecDestroy(e->hold_exec);
+  if (e->frame_exec) (void)hipGraphExecDestroy(e->frame_exec);
+  if (e->warena) (void)hipFree(e->warena);
+  if (e->kv) (void)hipFree(e->kv);
+  if (e->aarena) (void)hipFree(e->aarena);
+  if (e->ev0) (void)hipEventDestroy(e->ev0);
+  if (e->ev1) (void)hipEventDestroy(e->ev1);
+  if (e->st) (void)hipStreamDestroy(e->st);
+  delete e;
+}
+
+int vx_load_tensor(vx_engine *e, const char *name, const uint16_t *f16, size_t numel,
+                   const int64_t *shape, int32_t ndim) {
+  if (!e || !name || !f16) return e ? fail(e, VX_E_INVALID, "NULL argument") : VX_E_INVALID;
+  auto it = e->slots.find(name);
+  if (it == e->slots.end()) return fail(e, VX_E_INVALID, "Unknown tensor: %s", name);
+  Slot &s = it->second;
+  if (numel != s.numel) return fail(e, VX_E_INVALID, "%s: %zu elements, expected %zu", name, numel, s.numel);
+  if (shape) {
+    if ((size_t)ndim != s.shape.size())
+      return fail(e, VX_E_INVALID, "%s: rank %d, expected %zu", name, ndim, s.shape.size());
+    for (int i = 0; i < ndim; i++)
+      if (shape[i] != s.shape[i]) return fail(e, VX_E_INVALID, "%s: shape mismatch in dim %d", name, i);
+  }
+  HIPCHK(e, hipMemcpyAsync(s.ptr, f16, numel * 2, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  s.loaded = true;
+  if (s.ptr == e->fm_time) e->tproj_ready = false;
+  return VX_OK;
+}
+
+int vx_init_synthetic(vx_engine *e, uint64_t seed, float std) {
+  if (!e) return VX_E_INVALID;
+  for (auto &kv : e->slots) {
+    Slot &s = kv.second;
+    size_t blocks = std::min<size_t>((s.numel + 255) / 256, 65536);
+    hipLaunchKernelGGL(gen_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, e->st, s.ptr, s.numel,
+                       seed, fnv1a(kv.first.c_str()), s.is_norm ? 1.0f : 0.0f, std);
+    s.loaded = true;
+  }
+  LAUNCHCHK(e);
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  e->tproj_ready = false;
+  return VX_OK;
+}
+
+int vx_is_ready(const vx_engine *e) {
+  if (!e) return 0;
+  for (auto &kv : e->slots)
+    if (!kv.second.loaded) return 0;
+  return 1;
+}
+
+int vx_set_position(vx_engine *e, int32_t p) {
+  if (!e) return VX_E_INVALID;
+  if (p < 0 || p > e->max_seq) return fail(e, VX_E_RANGE, "position %d out of range", p);
+  hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, e->st, e->pos, p);
+  LAUNCHCHK(e);
+  e->host_pos = p;
+  return VX_OK;
+}
+
+int vx_reset(vx_engine *e) {
+  if (!e) return VX_E_INVALID;
+  hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, e->st, e->frame, 0);
+  return vx_set_position(e, 0);
+}
+
+int32_t vx_position(const vx_engine *e) { return e ? e->host_pos : -1; }
+
+int vx_synchronize(vx_engine *e) {
+  if (!e) return VX_E_INVALID;
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+int vx_backbone_step(vx_engine *e, int32_t token, int32_t mode, const float *pre, int32_t lm_head,
+                     uint32_t *argmax_out, float *normed_out) {
+  if (!e) return VX_E_INVALID;
+  int rc = check_ready(e);
+  if (rc) return rc;
+  if ((rc = ensure_graphs(e))) return rc;
+  if ((rc = prepare_input(e, token, mode, pre))) return rc;
+  HIPCHK(e, hipGraphLaunch(e->step_exec, e->st));
+  e->host_pos++;
+  if (lm_head) {
+    enqueue_lm_head(e);
+    LAUNCHCHK(e);
+  }
+  if (argmax_out && lm_head)
+    HIPCHK(e, hipMemcpyAsync(argmax_out, e->argmax_res, 4, hipMemcpyDeviceToHost, e->st));
+  if (normed_out)
+    HIPCHK(e, hipMemcpyAsync(normed_out, e->normed, DIM * 4, hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+int vx_backbone_step_layers(vx_engine *e, int32_t token, int32_t mode, const float *pre,
+                            float *layer_out) {
+  if (!e || !layer_out) return VX_E_INVALID;
+  int rc = check_ready(e);
+  if (rc) return rc;
+  if ((rc = prepare_input(e, token, mode, pre))) return rc;
+  for (int l = 0; l < e->cfg.n_layers; l++) {
+    enqueue_layer(e, l, VX_KERNEL_QKV);
+    enqueue_layer(e, l, VX_KERNEL_ATTN);
+    enqueue_layer(e, l, VX_KERNEL_OPROJ);
+    HIPCHK(e, hipMemcpyAsync(e->layer_stage + (size_t)(2 * l) * DIM, e->x, DIM * 4,
+                             hipMemcpyDeviceToDevice, e->st));
+    enqueue_layer(e, l, VX_KERNEL_GATEUP);
+    enqueue_layer(e, l, VX_KERNEL_DOWN);
+    HIPCHK(e, hipMemcpyAsync(e->layer_stage + (size_t)(2 * l + 1) * DIM, e->x, DIM * 4,
+                             hipMemcpyDeviceToDevice, e->st));
+  }
+  hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->final_norm,
+                     e->cfg.norm_eps, e->normed, e->pos);
+  LAUNCHCHK(e);
+  e->host_pos++;
+  HIPCHK(e, hipMemcpyAsync(layer_out, e->layer_stage, (size_t)e->cfg.n_layers * 2 * DIM * 4,
+                           hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+int vx_fm_forward(vx_engine *e, const float *noise, float *sem_logits, uint32_t *codes,
+                  float *x_final) {
+  if (!e) return VX_E_INVALID;
+  int rc = check_ready(e);
+  if (rc) return rc;
+  if ((rc = ensure_tproj(e))) return rc;
+  if (noise) {
+    HIPCHK(e, hipMemcpyAsync(e->noise, noise, NAC * 4, hipMemcpyHostToDevice, e->st));
+  } else {
+    hipLaunchKernelGGL(fm_noise_kernel, dim3(1), dim3(64), 0, e->st, e->noise, e->noise_seed,
+                       kNoiseStream, e->frame);
+  }
+  enqueue_fm(e, e->noise, false);
+  LAUNCHCHK(e);
+  if (sem_logits)
+    HIPCHK(e, hipMemcpyAsync(sem_logits, e->sem_logits, SEMV * 4, hipMemcpyDeviceToHost, e->st));
+  if (codes) HIPCHK(e, hipMemcpyAsync(codes, e->codes, NAC * 4, hipMemcpyDeviceToHost, e->st));
+  if (x_final)
+    HIPCHK(e, hipMemcpyAsync(x_final, e->xh + (size_t)e->nsteps() * NAC, NAC * 4,
+                             hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+int vx_set_semantic_code(vx_engine *e, uint32_t code) {
+  if (!e) return VX_E_INVALID;
+  if ((int)code >= e->cfg.audio_vocab) return fail(e, VX_E_INVALID, "semantic code %u out of range", code);
+  hipLaunchKernelGGL(set_u32_kernel, dim3(1), dim3(1), 0, e->st, e->sem_code, code);
+  LAUNCHCHK(e);
+  return VX_OK;
+}
+
+int vx_set_acoustic_codes(vx_engine *e, const uint32_t *c) {
+  if (!e || !c) return VX_E_INVALID;
+  for (int i = 0; i < NAC; i++)
+    if (c[i] > 22) return fail(e, VX_E_INVALID, "acoustic code %u out of range", c[i]);
+  HIPCHK(e, hipMemcpyAsync(e->codes, c, NAC * 4, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+int vx_get_codes(vx_engine *e, uint32_t *sem, uint32_t *c) {
+  if (!e) return VX_E_INVALID;
+  if (sem) HIPCHK(e, hipMemcpyAsync(sem, e->sem_code, 4, hipMemcpyDeviceToHost, e->st));
+  if (c) HIPCHK(e, hipMemcpyAsync(c, e->codes, NAC * 4, hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+int vx_read(vx_engine *e, const char *name, float *dst, size_t count) {
+  if (!e || !name || !dst) return VX_E_INVALID;
+  struct B {
+    const char *n;
+    const float *p;
+    size_t cnt;
+  } t[] = {
+      {"hidden", e->x, DIM},
+      {"normed", e->normed, DIM},
+      {"q", e->q, QD},
+      {"attn_out", e->attn, QD},
+      {"gate", e->act, HID},
+      {"logits", e->logits, (size_t)e->cfg.vocab_size},
+      {"semantic_logits", e->sem_logits, SEMV},
+      {"x_t", e->xh + (size_t)e->nsteps() * NAC, NAC},
+      {"velocity", e->vel + (size_t)(e->nsteps() - 1) * 2 * NAC, NAC},
+      {"v_uncond", e->vel + (size_t)(e->nsteps() - 1) * 2 * NAC + NAC, NAC},
+      {"fm_hidden", e->fm_llm_out, DIM},
+      {"fm_seq", e->fm_seq, 6 * DIM},
+      {"time_proj", e->tproj, (size_t)e->nsteps() * DIM},
+      {"x_history", e->xh, (size_t)(e->nsteps() + 1) * NAC},
+      {"velocity_history", e->vel, (size_t)e->nsteps() * 2 * NAC},
+  };
+  for (auto &b : t)
+    if (!strcmp(b.n, name)) {
+      if (count > b.cnt) return fail(e, VX_E_INVALID, "%s holds %zu values", name, b.cnt);
+      HIPCHK(e, hipMemcpyAsync(dst, b.p, count * 4, hipMemcpyDeviceToHost, e->st));
+      HIPCHK(e, hipStreamSynchronize(e->st));
+      return VX_OK;
+    }
+  return fail(e, VX_E_INVALID, "Unknown buffer: %s", name);
+}
+
+int vx_write(vx_engine *e, const char *name, const float *src, size_t count) {
+  if (!e || !name || !src) return VX_E_INVALID;
+  float *dst = nullptr;
+  if (!strcmp(name, "normed")) dst = e->normed;
+  else if (!strcmp(name, "hidden")) dst = e->x;
+  else return fail(e, VX_E_INVALID, "Unknown writable buffer: %s", name);
+  if (count > (size_t)DIM) return fail(e, VX_E_INVALID, "%s holds %d values", name, DIM);
+  HIPCHK(e, hipMemcpyAsync(dst, src, count * 4, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+static int kv_io(vx_engine *e, int32_t layer, int32_t which, int32_t pos0, int32_t npos,
+                 uint16_t *host, bool write) {
+  if (!e || !host) return VX_E_INVALID;
+  if (layer < 0 || layer >= e->cfg.n_layers || which < 0 || which > 1 || pos0 < 0 || npos < 0 ||
+      pos0 + npos > e->max_seq)
+    return fail(e, VX_E_INVALID, "KV range out of bounds");
+  uint16_t *base = which ? e->vc(layer) : e->kc(layer);
+  // caller layout [pos][kvh*128 + d] <-> device [kvh][pos][d]: one 2D copy per head
+  for (int h = 0; h < NKV; h++) {
+    uint16_t *dev = base + ((size_t)h * e->max_seq + pos0) * HD;
+    uint16_t *hp = host + h * HD;
+    if (write)
+      HIPCHK(e, hipMemcpy2DAsync(dev, HD * 2, hp, KVD * 2, HD * 2, npos, hipMemcpyHostToDevice, e->st));
+    else
+      HIPCHK(e, hipMemcpy2DAsync(hp, KVD * 2, dev, HD * 2, HD * 2, npos, hipMemcpyDeviceToHost, e->st));
+  }
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+int vx_write_kv(vx_engine *e, int32_t layer, int32_t which, int32_t pos0, int32_t npos,
+                const uint16_t *f16) {
+  return kv_io(e, layer, which, pos0, npos, const_cast<uint16_t *>(f16), true);
+}
+
+int vx_read_kv(vx_engine *e, int32_t layer, int32_t which, int32_t pos0, int32_t npos, uint16_t *f16) {
+  return kv_io(e, layer, which, pos0, npos, f16, false);
+}
+
+int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos) {
+  if (!e) return VX_E_INVALID;
+  if (npos < 0 || npos > e->max_seq) return fail(e, VX_E_INVALID, "npos out of range");
+  for (int l = 0; l < e->cfg.n_layers; l++)
+    for (int w = 0; w < 2; w++) {
+      std::string nm = "kv." + std::to_string(l) + (w ? ".v" : ".k");
+      hipLaunchKernelGGL(gen_kv_kernel, dim3(1024), dim3(256), 0, e->st, w ? e->vc(l) : e->kc(l),
+                         e->max_seq, npos, seed, fnv1a(nm.c_str()));
+    }
+  LAUNCHCHK(e);
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+// ------------------------------------------------------------- generate
+void vx_generate_options_default(vx_generate_options *o) {
+  if (!o) return;
+  o->sampling = VX_SAMPLE_TOP_P;
+  o->top_p = 0.9f;
+  o->temperature = 0.8f;
+  o->seed = 0;
+  o->ignore_eos = 0;
+}
+
+// sampleTopP, src/engine.ts:247-289, with a seeded uniform in place of
+// Math.random.  Float32Array intermediates, double accumulators, stable
+// descending sort, as the TypeScript does.
+static uint32_t sample_top_p(const float *logits, int n, float top_p, float temp, uint64_t *rng) {
+  std::vector<float> sc(n);
+  for (int i = 0; i < n; i++) sc[i] = (float)((double)logits[i] / (double)temp);
+  double mx = -INFINITY;
+  for (int i = 0; i < n; i++)
+    if (sc[i] > mx) mx = sc[i];
+  double sum = 0;
+  for (int i = 0; i < n; i++) {
+    sc[i] = (float)std::exp((double)sc[i] - mx);
+    sum += sc[i];
+  }
+  for (int i = 0; i < n; i++) sc[i] = (float)((double)sc[i] / sum);
+  std::vector<int> idx(n);
+  std::iota(idx.begin(), idx.end(), 0);
+  std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return sc[b] < sc[a]; });
+  double cum = 0;
+  int cutoff = n;
+  for (int i = 0; i < n; i++) {
+    cum += sc[idx[i]];
+    if (cum >= top_p) {
+      cutoff = i + 1;
+      break;
+    }
+  }
+  double resum = 0;
+  for (int i = 0; i < cutoff; i++) resum += sc[idx[i]];
+  *rng += 0x9E3779B97F4A7C15ull;
+  uint64_t z = *rng;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  double r = (double)(z >> 11) * 0x1p-53 * resum;
+  double acc = 0;
+  for (int i = 0; i < cutoff; i++) {
+    acc += sc[idx[i]];
+    if (acc >= r) return (uint32_t)idx[i];
+  }
+  return (uint32_t)idx[0];
+}
+
+int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t audio_start,
+                int32_t audio_count, const float *voice, int32_t max_frames,
+                const vx_generate_options *opt_in, vx_frame_cb on_frame, vx_stage_cb on_stage,
+                void *user, uint32_t *sem_out, uint32_t *ac_out, vx_generate_stats *stats) {
+  if (!e) return VX_E_INVALID;
+  int rc = check_ready(e);
+  if (rc) return fail(e, VX_E_STATE, "Engine not initialized. Call init() and loadWeights() first.");
+  if (n_tokens < 0 || (n_tokens > 0 && !tokens) || max_frames < 0)
+    return fail(e, VX_E_INVALID, "bad arguments");
+  if (n_tokens + 1 + (max_frames > 0 ? max_frames - 1 : 0) > e->max_seq)
+    return fail(e, VX_E_RANGE, "prompt + frames exceed max_seq_len %d", e->max_seq);
+  vx_generate_options opt;
+  vx_generate_options_default(&opt);
+  if (opt_in) opt = *opt_in;
+  using clk = std::chrono::steady_clock;
+  auto ms = [](clk::time_point a, clk::time_point b) {
+    return std::chrono::duration<double, std::milli>(b - a).count();
+  };
+  if ((rc = vx_reset(e))) return rc;
+  HIPCHK(e, hipMemcpyAsync(e->noise_seed, &opt.seed, 8, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  auto t0 = clk::now();
+  if (on_stage) on_stage(user, 0, -1.0);
+  if ((rc = ensure_graphs(e)) || (rc = ensure_tproj(e))) return rc;
+  // prefill, one token per step (src/engine.ts:2457-2472); the LM head the
+  // reference runs per prefill token is never read, so it is skipped
+  for (int i = 0; i < n_tokens; i++) {
+    bool is_voice = voice && i >= audio_start && i < audio_start + audio_count;
+    if ((rc = prepare_input(e, tokens[i], is_voice ? VX_EMBED_PRECOMPUTED : VX_EMBED_TOKEN,
+                            is_voice ? voice + (size_t)(i - audio_start) * DIM : nullptr)))
+      return rc;
+    HIPCHK(e, hipGraphLaunch(e->step_exec, e->st));
+    e->host_pos++;
+  }
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  auto t1 = clk::now();
+  if (on_stage) {
+    on_stage(user, 0, ms(t0, t1));
+    on_stage(user, 1, -1.0);
+  }
+  // AUDIO token kick (src/engine.ts:2478-2487)
+  if ((rc = prepare_input(e, 24, VX_EMBED_TOKEN, nullptr))) return rc;
+  HIPCHK(e, hipGraphLaunch(e->step_exec, e->st));
+  e->host_pos++;
+
+  uint64_t rng = opt.seed ^ 0x5bd1e9955bd1e995ull;
+  std::vector<float> logits(SEMV);
+  uint32_t codes[NAC];
+  int frames = 0;
+  for (int f = 0; f < max_frames; f++) {
+    if (f > 0) {
+      if ((rc = prepare_input(e, 0, VX_EMBED_CODES, nullptr))) return rc;
+      HIPCHK(e, hipGraphLaunch(e->step_exec, e->st));
+      e->host_pos++;
+    }
+    hipLaunchKernelGGL(fm_noise_kernel, dim3(1), dim3(64), 0, e->st, e->noise, e->noise_seed,
+                       kNoiseStream, e->frame);
+    const bool greedy = opt.sampling == VX_SAMPLE_GREEDY;
+    enqueue_fm(e, e->noise, greedy);
+    LAUNCHCHK(e);
+    uint32_t code;
+    if (greedy) {
+      HIPCHK(e, hipMemcpyAsync(&code, e->sem_code, 4, hipMemcpyDeviceToHost, e->st));
+      HIPCHK(e, hipStreamSynchronize(e->st));
+    } else {
+      HIPCHK(e, hipMemcpyAsync(logits.data(), e->sem_logits, SEMV * 4, hipMemcpyDeviceToHost, e->st));
+      HIPCHK(e, hipStreamSynchronize(e->st));
+      logits[0] = -INFINITY;  // src/engine.ts:2559-2563
+      for (int i = 8194; i < SEMV; i++) logits[i] = -INFINITY;
+      code = sample_top_p(logits.data(), SEMV, opt.top_p, opt.temperature, &rng);
+    }
+    if (code <= 1 && !opt.ignore_eos) break;
+    if (!greedy) {
+      hipLaunchKernelGGL(set_u32_kernel, dim3(1), dim3(1), 0, e->st, e->sem_code, code);
+      LAUNCHCHK(e);
+    }
+    HIPCHK(e, hipMemcpyAsync(codes, e->codes, NAC * 4, hipMemcpyDeviceToHost, e->st));
+    HIPCHK(e, hipStreamSynchronize(e->st));
+    if (sem_out) sem_out[f] = code;
+    if (ac_out) memcpy(ac_out + (size_t)f * NAC, codes, sizeof codes);
+    frames++;
+    if (on_frame) on_frame(user, f, code, codes);
+  }
+  auto t2 = clk::now();
+  if (on_stage) {
+    on_stage(user, 1, ms(t1, t2));
+    on_stage(user, 2, -1.0);
+    on_stage(user, 2, 0.0);
+  }
+  if (stats) {
+    stats->backbone_ms = ms(t0, t1);
+    stats->fm_ms = ms(t1, t2);
+    stats->codec_ms = 0;
+    stats->total_ms = ms(t0, t2);
+    stats->frames_generated = frames;
+  }
+  return VX_OK;
+}
+
+// ---------------------------------------------------------- measurement
+int vx_time_backbone_steps(vx_engine *e, int32_t n, int32_t hold, float *out_ms) {
+  if (!e || n < 1 || !out_ms) return VX_E_INVALID;
+  int rc = check_ready(e);
+  if (rc) return rc;
+  if (e->host_pos + (hold ? 1 : n) > e->max_seq) return fail(e, VX_E_RANGE, "steps pass max_seq_len");
+  if ((rc = ensure_graphs(e))) return rc;
+  if (hold && !e->hold_exec && (rc = capture(e, &e->hold_exec, enqueue_backbone_hold))) return rc;
+  hipGraphExec_t g = hold ? e->hold_exec : e->step_exec;
+  HIPCHK(e, hipEventRecord(e->ev0, e->st));
+  for (int i = 0; i < n; i++) HIPCHK(e, hipGraphLaunch(g, e->st));
+  HIPCHK(e, hipEventRecord(e->ev1, e->st));
+  HIPCHK(e, hipEventSynchronize(e->ev1));
+  if (!hold) e->host_pos += n;
+  HIPCHK(e, hipEventElapsedTime(out_ms, e->ev0, e->ev1));
+  return VX_OK;
+}
+
+int vx_time_frames(vx_engine *e, int32_t n, float *out_ms) {
+  if (!e || n < 1 || !out_ms) return VX_E_INVALID;
+  int rc = check_ready(e);
+  if (rc) return rc;
+  if (e->host_pos + n > e->max_seq) return fail(e, VX_E_RANGE, "frames pass max_seq_len");
+  if ((rc = ensure_tproj(e))) return rc;
+  if (!e->frame_exec && (rc = capture(e, &e->frame_exec, frame_body))) return rc;
+  HIPCHK(e, hipEventRecord(e->ev0, e->st));
+  for (int i = 0; i < n; i++) HIPCHK(e, hipGraphLaunch(e->frame_exec, e->st));
+  HIPCHK(e, hipEventRecord(e->ev1, e->st));
+  HIPCHK(e, hipEventSynchronize(e->ev1));
+  e->host_pos += n;
+  HIPCHK(e, hipEventElapsedTime(out_ms, e->ev0, e->ev1));
+  return VX_OK;
+}
+
+int vx_time_kernel(vx_engine *e, int32_t kernel, int32_t iters, float *avg_us, double *bytes) {
+  if (!e || iters < 1 || !avg_us || kernel < 0 || kernel > VX_KERNEL_DOWN) return VX_E_INVALID;
+  int rc = check_ready(e);
+  if (rc) return rc;
+  if (e->host_pos >= e->max_seq)
+    return fail(e, VX_E_RANGE, "position %d reaches max_seq_len %d", e->host_pos, e->max_seq);
+  const double seq = (double)e->host_pos + 1.0;
+  const double b[] = {
+      (double)QKV_ROWS * DIM * 2 + DIM * 2 + DIM * 4 + QD * 4 + 2 * KVD * 2,
+      seq * KVD * 2 * 2 + QD * 4 * 2,
+      (double)DIM * QD * 2 + QD * 4 + DIM * 8,
+      2.0 * HID * DIM * 2 + DIM * 2 + DIM * 4 + HID * 4,
+      (double)DIM * HID * 2 + HID * 4 + DIM * 8,
+  };
+  if (bytes) *bytes = b[kernel];
+  for (int i = 0; i < 2; i++) enqueue_layer(e, i % e->cfg.n_layers, kernel);  // warm-up
+  HIPCHK(e, hipEventRecord(e->ev0, e->st));
+  for (int i = 0; i < iters; i++) enqueue_layer(e, i % e->cfg.n_layers, kernel);
+  HIPCHK(e, hipEventRecord(e->ev1, e->st));
+  LAUNCHCHK(e);
+  HIPCHK(e, hipEventSynchronize(e->ev1));
+  float ms;
+  HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
+  *avg_us = ms * 1000.0f / iters;
+  return VX_OK;
+}
+
+}  // extern "C"

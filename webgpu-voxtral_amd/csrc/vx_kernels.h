@@ -1,0 +1,619 @@
+// vx_kernels.h -- HIP kernels of the MI355X (gfx950) Voxtral frame loop.
+//
+// Device layout (all in HBM, owned by the engine):
+//   weights   f16 row-major [out][in]; per backbone layer the Q, K and V
+//             projections are stacked into one [6144][3072] matrix.
+//   KV cache  f16 [layer][K|V][kv_head][max_seq][128] (head-major, so one
+//             split of one KV head reads a contiguous run of rows).
+//   activations f32.
+//
+// Kernels (each replaces one or more WGSL shaders of src/shaders.ts):
+//   gemv_kernel      matvecF16 (:21-71) and its Offset/Chunked forms, with
+//                    fused prologue (rmsNorm :137-183) and epilogues (rope
+//                    :224-256 + kvCacheWrite :452-473; addInPlace :532-547;
+//                    swiGLU :483-501).  NB input vectors share each weight
+//                    read (NB = 6 for the CFG-batched FM).
+//   attn_decode_kernel  attnScore/softmax/attnValue (:306-447) as split-K
+//                    flash decoding with a last-block log-sum-exp combine.
+//   fm_* kernels     biAttn* (:684-807), timeEmbedding (:579-602),
+//                    cfgCombine/eulerStep (:611-648), fsqQuantize (:653-673).
+//   argmax_kernel    argmax (:1154-1211), same 256-lane tree tie rule.
+//   embed kernels    embeddingLookup (:193-213), multiCodebookEmbed
+//                    (:1878-1917).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vx {
+
+constexpr int DIM = 3072;
+constexpr int HD = 128;
+constexpr int NH = 32;
+constexpr int NKV = 8;
+constexpr int QD = NH * HD;    // 4096
+constexpr int KVD = NKV * HD;  // 1024
+constexpr int HID = 9216;
+constexpr int QKV_ROWS = QD + 2 * KVD;  // 6144
+constexpr int NAC = 36;
+constexpr int SEMV = 8320;
+constexpr int ATTN_SPLITS = 32;  // split-K factor of the decode attention
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float h2f(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, RNE
+}
+
+// acc += sum_j w[j] * x[j] for 8 halves packed in a u32x4
+__device__ __forceinline__ float dot8(u32x4 w, f32x4 xa, f32x4 xb, float acc) {
+  h2 p0 = __builtin_bit_cast(h2, w.x), p1 = __builtin_bit_cast(h2, w.y),
+     p2 = __builtin_bit_cast(h2, w.z), p3 = __builtin_bit_cast(h2, w.w);
+  acc = fmaf((float)p0.x, xa.x, acc);
+  acc = fmaf((float)p0.y, xa.y, acc);
+  acc = fmaf((float)p1.x, xa.z, acc);
+  acc = fmaf((float)p1.y, xa.w, acc);
+  acc = fmaf((float)p2.x, xb.x, acc);
+  acc = fmaf((float)p2.y, xb.y, acc);
+  acc = fmaf((float)p3.x, xb.z, acc);
+  acc = fmaf((float)p3.y, xb.w, acc);
+  return acc;
+}
+
+// ------------------------------------------------------------------ GEMV
+enum Epi : int {
+  EPI_PLAIN = 0,   // out[b*os + row] = y
+  EPI_RESID = 1,   // out[b*os + row] += y   (residual add)
+  EPI_SWIGLU = 2,  // rows come in (W row i, W2 row i) pairs: out = silu(g)*u
+  EPI_QKV_ROPE = 3,// backbone: rope q,k at *pos; q -> out, k,v -> f16 cache
+  EPI_QKV = 4,     // FM: q -> out, k -> out_k, v -> out_v (no rope)
+};
+
+struct GemvArgs {
+  const uint16_t *W;   // [M][K]
+  const uint16_t *W2;  // SwiGLU up matrix [M][K]
+  const float *x;      // NB vectors, vector stride xs
+  int xs;
+  const uint16_t *norm_w;  // RMSNorm gains (NORM variants)
+  float eps;
+  float *out;  // output base, vector stride os
+  int os;
+  float *out_k, *out_v;  // EPI_QKV
+  int M;                 // rows (EPI_SWIGLU: row pairs)
+  // EPI_QKV_ROPE
+  const int *pos;
+  uint16_t *kc, *vc;  // this layer's K and V cache [NKV][max_seq][HD]
+  int max_seq;
+  float theta;
+};
+
+// Rows handled per wave = RPW (EPI_SWIGLU: RPW/2 pairs).  The block stages
+// the NB input vectors (RMS-normalised when NORM) into LDS one K-tile of KT
+// floats at a time; each lane streams 16-byte weight chunks, chunk c of a
+// row covering columns [c*512 + lane*8, +8), so a wave reads 1 KB of one
+// row per load instruction.
+template <int NB, int WAVES, int RPW, int EPI, bool NORM, int K, int KT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
+  static_assert(K % KT == 0 && KT % 512 == 0, "tile");
+  constexpr int NT = WAVES * 64;
+  constexpr int NCH = KT / 512;
+  __shared__ __attribute__((aligned(16))) float xl[NB * KT];
+  __shared__ float red[WAVES][NB];
+  __shared__ float scl[NB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int unit0 = (blockIdx.x * WAVES + wave) * (EPI == EPI_SWIGLU ? RPW / 2 : RPW);
+
+  if (NORM) {  // rmsNorm prologue: rms = 1/sqrt(mean(x^2) + eps)
+    float ss[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      float s = 0.f;
+      for (int i = tid * 4; i < K; i += NT * 4) {
+        f32x4 v = *(const f32x4 *)(a.x + (size_t)b * a.xs + i);
+        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+      ss[b] = wave_sum(s);
+    }
+    if (lane == 0)
+#pragma unroll
+      for (int b = 0; b < NB; b++) red[wave][b] = ss[b];
+    __syncthreads();
+    if (tid < NB) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; w++) s += red[w][tid];
+      scl[tid] = 1.0f / sqrtf(s / (float)K + a.eps);
+    }
+    __syncthreads();
+  }
+
+  float acc[RPW][NB];
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[r][b] = 0.f;
+
+  const bool active = unit0 < a.M;
+  for (int kt = 0; kt < K; kt += KT) {
+    if (kt) __syncthreads();
+    for (int i = tid * 4; i < NB * KT; i += NT * 4) {
+      int b = i / KT, k = i - b * KT;
+      f32x4 v = *(const f32x4 *)(a.x + (size_t)b * a.xs + kt + k);
+      if (NORM) {
+        float r = scl[b];
+        const uint16_t *g = a.norm_w + kt + k;
+        v.x = v.x * r * h2f(g[0]);
+        v.y = v.y * r * h2f(g[1]);
+        v.z = v.z * r * h2f(g[2]);
+        v.w = v.w * r * h2f(g[3]);
+      }
+      *(f32x4 *)(xl + i) = v;
+    }
+    __syncthreads();
+    if (active) {
+      u32x4 w[RPW][NCH];
+#pragma unroll
+      for (int r = 0; r < RPW; r++) {
+        const uint16_t *rowp;
+        if (EPI == EPI_SWIGLU)
+          rowp = ((r & 1) ? a.W2 : a.W) + (size_t)(unit0 + (r >> 1)) * K;
+        else
+          rowp = a.W + (size_t)min(unit0 + r, a.M - 1) * K;
+#pragma unroll
+        for (int c = 0; c < NCH; c++)
+          w[r][c] = __builtin_nontemporal_load(
+              (const u32x4 *)(rowp + kt + c * 512 + lane * 8));
+      }
+#pragma unroll
+      for (int c = 0; c < NCH; c++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          const float *xp = xl + b * KT + c * 512 + lane * 8;
+          f32x4 xa = *(const f32x4 *)xp, xb = *(const f32x4 *)(xp + 4);
+#pragma unroll
+          for (int r = 0; r < RPW; r++) acc[r][b] = dot8(w[r][c], xa, xb, acc[r][b]);
+        }
+    }
+  }
+  if (!active) return;
+
+#pragma unroll
+  for (int r = 0; r < RPW; r++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[r][b] = wave_sum(acc[r][b]);
+  if (lane != 0) return;
+
+  if (EPI == EPI_SWIGLU) {
+#pragma unroll
+    for (int r = 0; r < RPW; r += 2) {
+      int i = unit0 + r / 2;
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        float g = acc[r][b], u = acc[r + 1][b];
+        float silu = g / (1.0f + expf(-g));
+        a.out[(size_t)b * a.os + i] = silu * u;
+      }
+    }
+  } else if (EPI == EPI_QKV_ROPE) {
+    const int pos = *a.pos;
+#pragma unroll
+    for (int r = 0; r < RPW; r += 2) {
+      const int row = unit0 + r;  // even
+      float y0 = acc[r][0], y1 = acc[r + 1][0];
+      if (row < QD + KVD) {  // q or k: interleaved rope on (row, row+1)
+        int pair = (row & (HD - 1)) >> 1;
+        float freq = 1.0f / powf(a.theta, (float)(pair * 2) / (float)HD);
+        float ang = (float)pos * freq;
+        float cs = cosf(ang), sn = sinf(ang);
+        float r0 = y0 * cs - y1 * sn, r1 = y0 * sn + y1 * cs;
+        if (row < QD) {
+          a.out[row] = r0;
+          a.out[row + 1] = r1;
+        } else {
+          int c = row - QD, kvh = c >> 7, d = c & (HD - 1);
+          uint16_t *dst = a.kc + ((size_t)kvh * a.max_seq + pos) * HD + d;
+          dst[0] = f2h(r0);
+          dst[1] = f2h(r1);
+        }
+      } else {
+        int c = row - QD - KVD, kvh = c >> 7, d = c & (HD - 1);
+        uint16_t *dst = a.vc + ((size_t)kvh * a.max_seq + pos) * HD + d;
+        dst[0] = f2h(y0);
+        dst[1] = f2h(y1);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+      int row = unit0 + r;
+      if (row >= a.M) break;
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        float y = acc[r][b];
+        if (EPI == EPI_PLAIN) {
+          a.out[(size_t)b * a.os + row] = y;
+        } else if (EPI == EPI_RESID) {
+          float *o = a.out + (size_t)b * a.os + row;
+          *o = y + *o;
+        } else {  // EPI_QKV
+          if (row < QD)
+            a.out[(size_t)b * QD + row] = y;
+          else if (row < QD + KVD)
+            a.out_k[(size_t)b * KVD + row - QD] = y;
+          else
+            a.out_v[(size_t)b * KVD + row - QD - KVD] = y;
+        }
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------- decode attention
+struct AttnArgs {
+  const float *q;        // [NH*HD], roped
+  const uint16_t *kc;    // layer K cache [NKV][max_seq][HD]
+  const uint16_t *vc;
+  const int *pos;        // decode position; keys 0..pos
+  int max_seq;
+  float *part;           // [NH][ATTN_SPLITS][HD + 2] (o, m, l)
+  int *counter;          // [NKV] arrival counters, zero between launches
+  float *out;            // [NH*HD]
+};
+
+// grid (ATTN_SPLITS, NKV), 256 threads: wave w handles query head
+// 4*kv_head + w over this split's key range.  Scores use one lane per key
+// (q broadcast from LDS), values one lane per 2 dims.  The last block of a
+// KV head to finish merges the splits: M = max m_s, L = sum l_s e^(m_s-M),
+// o = sum o_s e^(m_s-M) / L.
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = kvh * (NH / NKV) + wave;
+  const int seq = *a.pos + 1;
+  const int chunk = (seq + ATTN_SPLITS - 1) / ATTN_SPLITS;
+  const int p0 = split * chunk, p1 = min(seq, p0 + chunk);
+  __shared__ __attribute__((aligned(16))) float qs[4][HD];
+  __shared__ float ps[4][64];
+  __shared__ int is_last;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  qs[wave][lane * 2] = a.q[h * HD + lane * 2];
+  qs[wave][lane * 2 + 1] = a.q[h * HD + lane * 2 + 1];
+  __syncthreads();
+
+  const uint16_t *Kb = a.kc + (size_t)kvh * a.max_seq * HD;
+  const uint16_t *Vb = a.vc + (size_t)kvh * a.max_seq * HD;
+  float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int pb = p0; pb < p1; pb += 64) {
+    const int p = pb + lane;
+    float s = -INFINITY;
+    if (p < p1) {
+      const u32x4 *kr = (const u32x4 *)(Kb + (size_t)p * HD);
+      float dot = 0.f;
+#pragma unroll
+      for (int c = 0; c < HD / 8; c++) {
+        u32x4 kv = kr[c];
+        f32x4 xa = *(const f32x4 *)&qs[wave][c * 8];
+        f32x4 xb = *(const f32x4 *)&qs[wave][c * 8 + 4];
+        dot = dot8(kv, xa, xb, dot);
+      }
+      s = dot * scale;
+    }
+    const float mnew = fmaxf(m, wave_max(s));
+    const float e = (p < p1) ? expf(s - mnew) : 0.f;
+    const float corr = expf(m - mnew);
+    l = l * corr + wave_sum(e);
+    o0 *= corr;
+    o1 *= corr;
+    ps[wave][lane] = e;
+    __builtin_amdgcn_wave_barrier();
+    const int n = min(64, p1 - pb);
+    const uint16_t *vp = Vb + (size_t)pb * HD + lane * 2;
+    int j = 0;
+    for (; j + 4 <= n; j += 4) {
+      uint32_t v0 = *(const uint32_t *)(vp + (size_t)(j + 0) * HD);
+      uint32_t v1 = *(const uint32_t *)(vp + (size_t)(j + 1) * HD);
+      uint32_t v2 = *(const uint32_t *)(vp + (size_t)(j + 2) * HD);
+      uint32_t v3 = *(const uint32_t *)(vp + (size_t)(j + 3) * HD);
+      h2 a0 = __builtin_bit_cast(h2, v0), a1 = __builtin_bit_cast(h2, v1),
+         a2 = __builtin_bit_cast(h2, v2), a3 = __builtin_bit_cast(h2, v3);
+      float e0 = ps[wave][j], e1 = ps[wave][j + 1], e2 = ps[wave][j + 2], e3 = ps[wave][j + 3];
+      o0 = fmaf(e0, (float)a0.x, o0); o1 = fmaf(e0, (float)a0.y, o1);
+      o0 = fmaf(e1, (float)a1.x, o0); o1 = fmaf(e1, (float)a1.y, o1);
+      o0 = fmaf(e2, (float)a2.x, o0); o1 = fmaf(e2, (float)a2.y, o1);
+      o0 = fmaf(e3, (float)a3.x, o0); o1 = fmaf(e3, (float)a3.y, o1);
+    }
+    for (; j < n; j++) {
+      h2 v = __builtin_bit_cast(h2, *(const uint32_t *)(vp + (size_t)j * HD));
+      float ej = ps[wave][j];
+      o0 = fmaf(ej, (float)v.x, o0);
+      o1 = fmaf(ej, (float)v.y, o1);
+    }
+    __builtin_amdgcn_wave_barrier();
+    m = mnew;
+  }
+  float *pp = a.part + ((size_t)h * ATTN_SPLITS + split) * (HD + 2);
+  pp[lane * 2] = o0;
+  pp[lane * 2 + 1] = o1;
+  if (lane == 0) {
+    pp[HD] = m;
+    pp[HD + 1] = l;
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) is_last = (atomicAdd(&a.counter[kvh], 1) == ATTN_SPLITS - 1);
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  // merge: lane s < ATTN_SPLITS holds split s's (m, l)
+  const float *hp = a.part + (size_t)h * ATTN_SPLITS * (HD + 2);
+  float ms = -INFINITY, ls = 0.f;
+  if (lane < ATTN_SPLITS) {
+    ms = __builtin_nontemporal_load(hp + lane * (HD + 2) + HD);
+    ls = __builtin_nontemporal_load(hp + lane * (HD + 2) + HD + 1);
+  }
+  const float M = wave_max(ms);
+  const float wgt = (lane < ATTN_SPLITS) ? expf(ms - M) : 0.f;
+  const float L = wave_sum(ls * wgt);
+  float r0 = 0.f, r1 = 0.f;
+  for (int s = 0; s < ATTN_SPLITS; s++) {
+    float ws = __shfl(wgt, s, 64);
+    const float *op = hp + s * (HD + 2) + lane * 2;
+    r0 = fmaf(ws, __builtin_nontemporal_load(op), r0);
+    r1 = fmaf(ws, __builtin_nontemporal_load(op + 1), r1);
+  }
+  a.out[h * HD + lane * 2] = r0 / L;
+  a.out[h * HD + lane * 2 + 1] = r1 / L;
+  if (tid == 0) a.counter[kvh] = 0;
+}
+
+// ------------------------------------------------------- small kernels
+// embeddingLookup: out[i] = table[token][i]
+__global__ void embed_row_kernel(const uint16_t *table, int token, float *out) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < DIM) out[i] = h2f(table[(size_t)token * DIM + i]);
+}
+
+// multiCodebookEmbed: semantic row + 36 acoustic rows 8194 + k*23 + code_k,
+// summed in that order.
+__global__ void multi_codebook_kernel(const uint16_t *table, const uint32_t *sem,
+                                      const uint32_t *codes, float *out) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= DIM) return;
+  float s = 0.f;
+  s += h2f(table[(size_t)sem[0] * DIM + i]);
+  for (int k = 0; k < NAC; k++)
+    s += h2f(table[(size_t)(8194u + k * 23u + codes[k]) * DIM + i]);
+  out[i] = s;
+}
+
+// Final rmsNorm into `normed`; also advances the device decode position
+// after every kernel of the step has read it.
+__global__ __launch_bounds__(1024) void final_norm_kernel(const float *x, const uint16_t *w,
+                                                          float eps, float *normed, int *pos) {
+  __shared__ float red[16];
+  const int tid = threadIdx.x;
+  float s = 0.f;
+  for (int i = tid; i < DIM; i += 1024) s += x[i] * x[i];
+  s = wave_sum(s);
+  if ((tid & 63) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; k++) tot += red[k];
+  const float rms = 1.0f / sqrtf(tot / (float)DIM + eps);
+  for (int i = tid; i < DIM; i += 1024) normed[i] = x[i] * rms * h2f(w[i]);
+  if (pos != nullptr && tid == 0) *pos += 1;
+}
+
+// argmax with the reference's 256-lane strided scan and tree (strict '>').
+// mask_valid > 0: indices 0 and >= mask_valid count as -inf (the host-side
+// semantic masking of src/engine.ts:2556-2563).
+__global__ __launch_bounds__(256) void argmax_kernel(const float *x, int n, int mask_valid,
+                                                     uint32_t *result) {
+  __shared__ float bv[256];
+  __shared__ uint32_t bi[256];
+  const int t = threadIdx.x;
+  float best = -1e30f;
+  uint32_t idx = 0;
+  for (int i = t; i < n; i += 256) {
+    float v = x[i];
+    if (mask_valid > 0 && (i == 0 || i >= mask_valid)) v = -INFINITY;
+    if (v > best) {
+      best = v;
+      idx = (uint32_t)i;
+    }
+  }
+  bv[t] = best;
+  bi[t] = idx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (t < s && bv[t + s] > bv[t]) {
+      bv[t] = bv[t + s];
+      bi[t] = bi[t + s];
+    }
+    __syncthreads();
+  }
+  if (t == 0) result[0] = bi[0];
+}
+
+// ------------------------------------------------------------- generator
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+// Irwin-Hall(12) normal variate of (seed, stream, idx); bit-identical to
+// the CPU generator (integer arithmetic, one exact conversion).
+__device__ __forceinline__ float normal_variate(uint64_t seed, uint64_t stream, uint64_t idx) {
+  const uint64_t s0 = mix64(seed) ^ stream;
+  int64_t s = 0;
+#pragma unroll
+  for (uint64_t j = 0; j < 4; j++) {
+    uint64_t h = mix64(s0 + (4 * idx + j + 1) * 0x9E3779B97F4A7C15ull);
+    s += (int64_t)(h & 0xFFFFF) + (int64_t)((h >> 20) & 0xFFFFF) + (int64_t)((h >> 40) & 0xFFFFF);
+  }
+  return (float)(s - 6 * (int64_t)0xFFFFF) * 0x1p-20f;
+}
+
+__global__ void gen_f16_kernel(uint16_t *out, size_t n, uint64_t seed, uint64_t stream,
+                               float mean, float std) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    float t = __fmul_rn(normal_variate(seed, stream, i), std);
+    out[i] = f2h(__fadd_rn(mean, t));
+  }
+}
+
+// KV rows for positions [0, npos): element (pos, c) of the reference layout
+// [pos][1024] -> head-major cache [c/128][pos][c%128].
+__global__ void gen_kv_kernel(uint16_t *cache, int max_seq, int npos, uint64_t seed,
+                              uint64_t stream) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t n = (size_t)npos * KVD;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    int p = (int)(i / KVD), c = (int)(i % KVD);
+    cache[((size_t)(c >> 7) * max_seq + p) * HD + (c & 127)] = f2h(normal_variate(seed, stream, i));
+  }
+}
+
+// ------------------------------------------------------------- FM kernels
+// timeEmbedding (src/shaders.ts:579-602) for t
+__global__ void time_embed_kernel(float *out, float t) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int half = DIM / 2;
+  if (i >= half) return;
+  float freq = expf((float)-9.210340371976184 * (float)i / (float)half);
+  float ang = t * freq;
+  out[i] = cosf(ang);
+  out[half + i] = sinf(ang);
+}
+
+// CFG combine + Euler update (src/shaders.ts:611-648) of one coordinate:
+// v = alpha*v_c + (1-alpha)*v_u; x' = x + v*dt
+__device__ __forceinline__ float cfg_euler(float x, float vc, float vu, float alpha, float dt) {
+  float v = __fadd_rn(__fmul_rn(alpha, vc), __fmul_rn(1.0f - alpha, vu));
+  return __fadd_rn(x, __fmul_rn(v, dt));
+}
+
+struct FmStepArgs {
+  float *xh;          // x_t history [nfe][NAC]; row s is the input of step s
+  const float *vel;   // velocity history [nfe-1][2][NAC]
+  const uint16_t *w_in;  // input_projection [DIM][NAC]
+  const float *tproj;    // time projection of step s [DIM]
+  const float *llm;      // llm projection [DIM]
+  float *seq;            // [2][3][DIM]
+  int step;
+  float alpha, dt;
+  const float *noise;    // step 0: x_t = noise
+};
+
+// Start of Euler step s: x_s (from x_{s-1} and the CFG velocity of step
+// s-1, or the noise at s=0), x_t_proj = input_projection(x_s), and both CFG
+// sequences [x_t_proj, time_proj, llm | 0] (src/engine.ts:1292-1349).
+__global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
+  __shared__ float xs[NAC];
+  const int t = threadIdx.x;
+  if (t < NAC) {
+    float x;
+    if (a.step == 0) {
+      x = a.noise[t];
+    } else {
+      const float *vp = a.vel + (size_t)(a.step - 1) * 2 * NAC;
+      x = cfg_euler(a.xh[(a.step - 1) * NAC + t], vp[t], vp[NAC + t], a.alpha, a.dt);
+    }
+    xs[t] = x;
+    if (blockIdx.x == 0) a.xh[a.step * NAC + t] = x;
+  }
+  __syncthreads();
+  const int row = blockIdx.x * 256 + t;
+  if (row >= DIM) return;
+  const uint16_t *w = a.w_in + (size_t)row * NAC;
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < NAC; k++) acc = fmaf(h2f(w[k]), xs[k], acc);
+  float tp = a.tproj[row], lp = a.llm[row];
+  a.seq[0 * DIM + row] = acc;
+  a.seq[1 * DIM + row] = tp;
+  a.seq[2 * DIM + row] = lp;
+  a.seq[3 * DIM + row] = acc;
+  a.seq[4 * DIM + row] = tp;
+  a.seq[5 * DIM + row] = 0.f;
+}
+
+// Bidirectional 3-token GQA attention of both CFG branches: grid (NH, 2),
+// one wave per (head, branch); q [6][QD], k/v [6][KVD], out [6][QD].
+__global__ __launch_bounds__(64) void fm_attn_kernel(const float *q, const float *k,
+                                                     const float *v, float *out) {
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int kvh = h / (NH / NKV);
+  const float scale = 1.0f / sqrtf((float)HD);
+  float qv[3][2], kv[3][2], vv[3][2];
+#pragma unroll
+  for (int i = 0; i < 3; i++) {
+    const int vec = b * 3 + i;
+    qv[i][0] = q[(size_t)vec * QD + h * HD + lane * 2];
+    qv[i][1] = q[(size_t)vec * QD + h * HD + lane * 2 + 1];
+    kv[i][0] = k[(size_t)vec * KVD + kvh * HD + lane * 2];
+    kv[i][1] = k[(size_t)vec * KVD + kvh * HD + lane * 2 + 1];
+    vv[i][0] = v[(size_t)vec * KVD + kvh * HD + lane * 2];
+    vv[i][1] = v[(size_t)vec * KVD + kvh * HD + lane * 2 + 1];
+  }
+#pragma unroll
+  for (int i = 0; i < 3; i++) {
+    float s[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) s[j] = wave_sum(qv[i][0] * kv[j][0] + qv[i][1] * kv[j][1]) * scale;
+    float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+    float e0 = expf(s[0] - mx), e1 = expf(s[1] - mx), e2 = expf(s[2] - mx);
+    float sum = e0 + e1 + e2;
+    e0 /= sum; e1 /= sum; e2 /= sum;
+    const int vec = b * 3 + i;
+    out[(size_t)vec * QD + h * HD + lane * 2] = e0 * vv[0][0] + e1 * vv[1][0] + e2 * vv[2][0];
+    out[(size_t)vec * QD + h * HD + lane * 2 + 1] = e0 * vv[0][1] + e1 * vv[1][1] + e2 * vv[2][1];
+  }
+}
+
+// End of the Euler loop: last CFG/Euler update, then fsqQuantize (round
+// half to even) into the device acoustic codes; also advances the frame
+// counter of the noise generator.
+__global__ void fm_finish_kernel(float *xh, const float *vel, int last, float alpha, float dt,
+                                 uint32_t *codes, int levels, int *frame_counter) {
+  const int t = threadIdx.x;
+  if (t < NAC) {
+    const float *vp = vel + (size_t)last * 2 * NAC;
+    float x = cfg_euler(xh[last * NAC + t], vp[t], vp[NAC + t], alpha, dt);
+    xh[(last + 1) * NAC + t] = x;
+    float c = fminf(fmaxf(x, -1.0f), 1.0f);
+    float top = (float)(levels - 1);
+    float sc = rintf((c + 1.0f) * 0.5f * top);
+    codes[t] = (uint32_t)fminf(fmaxf(sc, 0.0f), top) + 2u;
+  }
+  if (t == 0 && frame_counter) *frame_counter += 1;
+}
+
+// Device noise: x_0[i] = normal(seed, stream, frame*36 + i)
+__global__ void fm_noise_kernel(float *noise, const uint64_t *seed, uint64_t stream,
+                                const int *frame_counter) {
+  const int t = threadIdx.x;
+  if (t < NAC) noise[t] = normal_variate(*seed, stream, (uint64_t)(*frame_counter) * NAC + t);
+}
+
+}  // namespace vx

@@ -1,0 +1,368 @@
+"""Python host binding of libvoxtral_amd.so (include/voxtral_engine.h).
+
+`VoxtralEngine` mirrors the public surface of the reference class
+(src/engine.ts:291-2633 of svenflow/webgpu-voxtral): same method names in
+snake_case, same argument meaning, same error messages.  Every call goes
+through the C ABI into the HIP engine; there is no CPU fallback -- importing
+works without a GPU, but creating an engine needs the built library and a
+HIP device, and fails loudly otherwise.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+LIB_PATH = os.path.join(PKG, "lib", "libvoxtral_amd.so")
+HEADER = os.path.join(os.path.dirname(PKG), "include", "voxtral_engine.h")
+
+VX_OK, VX_E_INVALID, VX_E_STATE, VX_E_DEVICE, VX_E_RANGE, VX_E_NOMEM = 0, -1, -2, -3, -4, -5
+EMBED_TOKEN, EMBED_AUDIO, EMBED_PRECOMPUTED, EMBED_CODES = 0, 1, 2, 3
+SAMPLE_TOP_P, SAMPLE_GREEDY = 0, 1
+KERNEL_QKV, KERNEL_ATTN, KERNEL_OPROJ, KERNEL_GATEUP, KERNEL_DOWN = range(5)
+KERNEL_NAMES = ["qkv", "attn", "oproj", "gateup", "down"]
+
+
+class VoxtralError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+class Config(ctypes.Structure):
+    """vx_config == defaultConfig (src/types.ts:70-122), backbone + fm."""
+    _fields_ = [
+        ("dim", ctypes.c_int32), ("n_layers", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("hidden_dim", ctypes.c_int32),
+        ("n_heads", ctypes.c_int32), ("n_kv_heads", ctypes.c_int32),
+        ("vocab_size", ctypes.c_int32), ("rope_theta", ctypes.c_float),
+        ("norm_eps", ctypes.c_float), ("fm_layers", ctypes.c_int32),
+        ("nfe", ctypes.c_int32), ("cfg_alpha", ctypes.c_float),
+        ("n_acoustic_out", ctypes.c_int32), ("semantic_vocab", ctypes.c_int32),
+        ("acoustic_levels", ctypes.c_int32), ("audio_vocab", ctypes.c_int32),
+    ]
+
+
+class GenerateOptions(ctypes.Structure):
+    _fields_ = [("sampling", ctypes.c_int32), ("top_p", ctypes.c_float),
+                ("temperature", ctypes.c_float), ("seed", ctypes.c_uint64),
+                ("ignore_eos", ctypes.c_int32)]
+
+
+class GenerateStats(ctypes.Structure):
+    _fields_ = [("backbone_ms", ctypes.c_double), ("fm_ms", ctypes.c_double),
+                ("codec_ms", ctypes.c_double), ("total_ms", ctypes.c_double),
+                ("frames_generated", ctypes.c_int32)]
+
+
+FRAME_CB = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32,
+                            ctypes.POINTER(ctypes.c_uint32))
+STAGE_CB = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int32, ctypes.c_double)
+
+_VP = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_SIGS = {
+    "vx_config_default": (_I32, [ctypes.POINTER(Config)]),
+    "vx_create": (_I32, [ctypes.POINTER(Config), _I32, ctypes.POINTER(_VP)]),
+    "vx_destroy": (None, [_VP]),
+    "vx_last_error": (ctypes.c_char_p, [_VP]),
+    "vx_load_tensor": (_I32, [_VP, ctypes.c_char_p, _VP, ctypes.c_size_t, _VP, _I32]),
+    "vx_init_synthetic": (_I32, [_VP, ctypes.c_uint64, ctypes.c_float]),
+    "vx_is_ready": (_I32, [_VP]),
+    "vx_reset": (_I32, [_VP]),
+    "vx_position": (_I32, [_VP]),
+    "vx_set_position": (_I32, [_VP, _I32]),
+    "vx_backbone_step": (_I32, [_VP, _I32, _I32, _VP, _I32, _VP, _VP]),
+    "vx_backbone_step_layers": (_I32, [_VP, _I32, _I32, _VP, _VP]),
+    "vx_fm_forward": (_I32, [_VP, _VP, _VP, _VP, _VP]),
+    "vx_set_semantic_code": (_I32, [_VP, ctypes.c_uint32]),
+    "vx_set_acoustic_codes": (_I32, [_VP, _VP]),
+    "vx_get_codes": (_I32, [_VP, _VP, _VP]),
+    "vx_read": (_I32, [_VP, ctypes.c_char_p, _VP, ctypes.c_size_t]),
+    "vx_write": (_I32, [_VP, ctypes.c_char_p, _VP, ctypes.c_size_t]),
+    "vx_write_kv": (_I32, [_VP, _I32, _I32, _I32, _I32, _VP]),
+    "vx_read_kv": (_I32, [_VP, _I32, _I32, _I32, _I32, _VP]),
+    "vx_fill_kv_synthetic": (_I32, [_VP, ctypes.c_uint64, _I32]),
+    "vx_generate_options_default": (None, [ctypes.POINTER(GenerateOptions)]),
+    "vx_generate": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP, _I32, ctypes.POINTER(GenerateOptions),
+                           FRAME_CB, STAGE_CB, _VP, _VP, _VP, ctypes.POINTER(GenerateStats)]),
+    "vx_time_backbone_steps": (_I32, [_VP, _I32, _I32, ctypes.POINTER(ctypes.c_float)]),
+    "vx_time_frames": (_I32, [_VP, _I32, ctypes.POINTER(ctypes.c_float)]),
+    "vx_time_kernel": (_I32, [_VP, _I32, _I32, ctypes.POINTER(ctypes.c_float),
+                              ctypes.POINTER(ctypes.c_double)]),
+    "vx_synchronize": (_I32, [_VP]),
+}
+
+_lib = None
+
+
+def load_library(path=None):
+    """Loads libvoxtral_amd.so; raises if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = path or LIB_PATH
+    if not os.path.exists(path):
+        raise RuntimeError(f"libvoxtral_amd.so not built ({path}); run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def default_config(**over):
+    c = Config()
+    load_library().vx_config_default(ctypes.byref(c))
+    for k, v in over.items():
+        setattr(c, k, v)
+    return c
+
+
+def _ptr(a):
+    return a.ctypes.data if a is not None else None
+
+
+def _f32(a, n=None):
+    a = np.ascontiguousarray(a, np.float32)
+    if n is not None and a.size != n:
+        raise ValueError(f"expected {n} float32 values, got {a.size}")
+    return a
+
+
+class VoxtralEngine:
+    """MI355X engine with the reference VoxtralEngine surface."""
+
+    def __init__(self, config=None, max_seq_len=4096):
+        self._lib = load_library()
+        self.config = config if config is not None else default_config()
+        self.max_seq_len = int(max_seq_len)
+        self._h = None
+
+    # -- lifecycle (constructor :301-304, init :313-340, destroy :2621) --
+    def init(self):
+        h = ctypes.c_void_p()
+        rc = self._lib.vx_create(ctypes.byref(self.config), self.max_seq_len, ctypes.byref(h))
+        if rc != VX_OK:
+            raise VoxtralError(rc, self._lib.vx_last_error(None).decode())
+        self._h = h
+        return self
+
+    def destroy(self):
+        if self._h:
+            self._lib.vx_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.destroy()
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc != VX_OK:
+            raise VoxtralError(rc, self._lib.vx_last_error(self._h).decode())
+
+    # -- weights (loadWeights :539, organizeWeights :659-743) --
+    def load_tensor(self, name, f16_bits, shape=None):
+        a = np.ascontiguousarray(f16_bits)
+        if a.dtype == np.float16:
+            a = a.view(np.uint16)
+        if a.dtype != np.uint16:
+            raise TypeError("weights are float16 (or their uint16 bit patterns)")
+        shape = tuple(shape) if shape is not None else a.shape
+        sh = (ctypes.c_int64 * len(shape))(*shape)
+        self._check(self._lib.vx_load_tensor(self._h, name.encode(), a.ctypes.data, a.size,
+                                             ctypes.cast(sh, ctypes.c_void_p), len(shape)))
+
+    def load_weights(self, tensors):
+        """tensors: mapping of reference tensor name -> float16 array."""
+        for name, arr in tensors.items():
+            self.load_tensor(name, arr)
+
+    def init_synthetic(self, seed=0, std=0.02):
+        self._check(self._lib.vx_init_synthetic(self._h, seed, std))
+
+    @property
+    def is_ready(self):
+        return bool(self._h) and bool(self._lib.vx_is_ready(self._h))
+
+    # -- state --
+    def reset(self):
+        self._check(self._lib.vx_reset(self._h))
+
+    @property
+    def position(self):
+        return self._lib.vx_position(self._h)
+
+    @position.setter
+    def position(self, p):
+        self._check(self._lib.vx_set_position(self._h, int(p)))
+
+    def write_kv(self, layer, which, pos0, f16_bits):
+        a = np.ascontiguousarray(f16_bits)
+        a = a.view(np.uint16) if a.dtype == np.float16 else a
+        kvd = self.config.n_kv_heads * self.config.head_dim
+        npos = a.size // kvd
+        self._check(self._lib.vx_write_kv(self._h, layer, which, pos0, npos, a.ctypes.data))
+
+    def read_kv(self, layer, which, pos0, npos):
+        kvd = self.config.n_kv_heads * self.config.head_dim
+        out = np.empty((npos, kvd), np.uint16)
+        self._check(self._lib.vx_read_kv(self._h, layer, which, pos0, npos, out.ctypes.data))
+        return out
+
+    def fill_kv_synthetic(self, seed, npos):
+        self._check(self._lib.vx_fill_kv_synthetic(self._h, seed, npos))
+
+    # -- backbone (backboneStep :814-1042) --
+    def backbone_step(self, token=0, mode=EMBED_TOKEN, precomputed=None, lm_head=False,
+                      read_normed=True):
+        pre = None
+        if precomputed is not None:
+            pre = _f32(precomputed, self.config.dim)
+            mode = EMBED_PRECOMPUTED
+        am = np.zeros(1, np.uint32)
+        normed = np.empty(self.config.dim, np.float32) if read_normed else None
+        self._check(self._lib.vx_backbone_step(self._h, int(token), int(mode), _ptr(pre),
+                                               int(bool(lm_head)), _ptr(am), _ptr(normed)))
+        return (int(am[0]) if lm_head else None), normed
+
+    def backbone_step_and_read(self, token_id, use_audio_embedding=False):
+        """backboneStepAndRead (:2333-2342): next-token argmax."""
+        am, _ = self.backbone_step(token_id, EMBED_AUDIO if use_audio_embedding else EMBED_TOKEN,
+                                   lm_head=True, read_normed=False)
+        return am
+
+    def debug_backbone_step_full(self, token_id, use_audio_embedding=False):
+        """debugBackboneStepFull (:2348-2357): final-norm hidden state."""
+        return self.backbone_step(token_id, EMBED_AUDIO if use_audio_embedding else EMBED_TOKEN)[1]
+
+    def debug_backbone_layer_by_layer(self, token_id, precomputed=None):
+        """debugBackboneLayerByLayer (:2106-2287) read points: hidden after
+        each attention residual and after each FFN residual, + final norm."""
+        c = self.config
+        out = np.empty((c.n_layers, 2, c.dim), np.float32)
+        pre = _f32(precomputed, c.dim) if precomputed is not None else None
+        mode = EMBED_PRECOMPUTED if pre is not None else EMBED_TOKEN
+        self._check(self._lib.vx_backbone_step_layers(self._h, int(token_id), mode, _ptr(pre),
+                                                      out.ctypes.data))
+        return {"layers": [{"attn_out": out[i, 0], "ffn_out": out[i, 1]} for i in range(c.n_layers)],
+                "final_norm": self.debug_read("normed", c.dim), "hidden": out[-1, 1]}
+
+    # -- FM (fmForward :1240-1380) --
+    def debug_fm_step(self, debug_noise=None):
+        """debugFMStep (:2363-2380)."""
+        noise = _f32(debug_noise, 36) if debug_noise is not None else None
+        sem = np.empty(self.config.semantic_vocab, np.float32)
+        codes = np.empty(36, np.uint32)
+        xf = np.empty(36, np.float32)
+        self._check(self._lib.vx_fm_forward(self._h, _ptr(noise), sem.ctypes.data,
+                                            codes.ctypes.data, xf.ctypes.data))
+        return {"semantic_logits": sem, "acoustic_codes": codes, "x_final": xf}
+
+    def fm_step_and_read(self):
+        """fmStepAndRead (:2386-2396): acoustic codes of one frame."""
+        codes = np.empty(36, np.uint32)
+        self._check(self._lib.vx_fm_forward(self._h, None, None, codes.ctypes.data, None))
+        return codes
+
+    def set_semantic_code(self, code):
+        self._check(self._lib.vx_set_semantic_code(self._h, int(code)))
+
+    def set_acoustic_codes(self, codes):
+        c = np.ascontiguousarray(codes, np.uint32)
+        self._check(self._lib.vx_set_acoustic_codes(self._h, c.ctypes.data))
+
+    def get_codes(self):
+        s = np.zeros(1, np.uint32)
+        c = np.zeros(36, np.uint32)
+        self._check(self._lib.vx_get_codes(self._h, s.ctypes.data, c.ctypes.data))
+        return int(s[0]), c
+
+    def debug_read(self, buffer_name, count=16):
+        """debugRead (:2062-2067)."""
+        out = np.empty(int(count), np.float32)
+        self._check(self._lib.vx_read(self._h, buffer_name.encode(), out.ctypes.data, out.size))
+        return out
+
+    def debug_write(self, buffer_name, values):
+        """queue.writeBuffer into `normed` or `hidden` (teacher forcing)."""
+        v = _f32(values)
+        self._check(self._lib.vx_write(self._h, buffer_name.encode(), v.ctypes.data, v.size))
+
+    # -- generate (:2416-2616) --
+    def generate(self, tokens, audio_token_start, audio_token_count, voice_embeddings,
+                 max_frames=500, on_frame=None, on_stage=None, sampling="top_p", seed=0,
+                 top_p=0.9, temperature=0.8, ignore_eos=False):
+        toks = np.ascontiguousarray(tokens, np.int32)
+        voice = None
+        if voice_embeddings is not None and audio_token_count > 0:
+            voice = _f32(voice_embeddings)
+            if voice.size < audio_token_count * self.config.dim:
+                raise ValueError("voiceEmbeddings shorter than audioTokenCount rows")
+        opt = GenerateOptions()
+        self._lib.vx_generate_options_default(ctypes.byref(opt))
+        opt.sampling = SAMPLE_GREEDY if sampling == "greedy" else SAMPLE_TOP_P
+        opt.top_p, opt.temperature, opt.seed, opt.ignore_eos = top_p, temperature, seed, int(ignore_eos)
+        sem = np.zeros(max(1, max_frames), np.uint32)
+        ac = np.zeros((max(1, max_frames), 36), np.uint32)
+        stages = ["backbone", "fm", "codec"]
+
+        def _frame(user, f, s, codes):
+            if on_frame:
+                on_frame(f, s, np.ctypeslib.as_array(codes, (36,)).copy())
+
+        def _stage(user, st, done):
+            if on_stage:
+                on_stage(stages[st], None if done < 0 else done)
+
+        fcb, scb = FRAME_CB(_frame), STAGE_CB(_stage)
+        stats = GenerateStats()
+        self._check(self._lib.vx_generate(self._h, toks.ctypes.data, toks.size, audio_token_start,
+                                          audio_token_count, _ptr(voice), max_frames,
+                                          ctypes.byref(opt), fcb, scb, None, sem.ctypes.data,
+                                          ac.ctypes.data, ctypes.byref(stats)))
+        n = stats.frames_generated
+        return {
+            "semanticCodes": [int(v) for v in sem[:n]],
+            "acousticCodes": [list(map(int, r)) for r in ac[:n]],
+            "audio": np.zeros(0, np.float32),  # codec decoder is outside this library
+            "stats": {"backboneMs": stats.backbone_ms, "fmMs": stats.fm_ms,
+                      "codecMs": stats.codec_ms, "totalMs": stats.total_ms,
+                      "framesGenerated": n},
+        }
+
+    # -- measurement (no reference counterpart) --
+    def time_backbone_steps(self, n, hold_position=False):
+        ms = ctypes.c_float()
+        self._check(self._lib.vx_time_backbone_steps(self._h, int(n), int(bool(hold_position)),
+                                                     ctypes.byref(ms)))
+        return ms.value
+
+    def time_frames(self, n):
+        ms = ctypes.c_float()
+        self._check(self._lib.vx_time_frames(self._h, int(n), ctypes.byref(ms)))
+        return ms.value
+
+    def time_kernel(self, kernel, iters):
+        us, b = ctypes.c_float(), ctypes.c_double()
+        self._check(self._lib.vx_time_kernel(self._h, int(kernel), int(iters), ctypes.byref(us),
+                                             ctypes.byref(b)))
+        return us.value, b.value
+
+    def synchronize(self):
+        self._check(self._lib.vx_synchronize(self._h))
