@@ -84,6 +84,10 @@ int vx_load_tensor(vx_engine *e, const char *name, const uint16_t *f16,
  * CPU oracle's generator. */
 int vx_init_synthetic(vx_engine *e, uint64_t seed, float std);
 
+/* Copies a loaded weight back to the host (no reference counterpart; test
+ * plumbing for generator and loader checks). */
+int vx_read_tensor(vx_engine *e, const char *name, uint16_t *f16, size_t numel);
+
 /* isReady getter, src/engine.ts:2047-2049.  1 when every weight is loaded. */
 int vx_is_ready(const vx_engine *e);
 

@@ -80,6 +80,7 @@ def lib():
             "vxo_weight": (c_vp, [c_vp, ctypes.c_char_p]),
             "vxo_is_ready": (c_int, [c_vp]),
             "vxo_reset": (None, [c_vp]),
+            "vxo_set_kv_f16": (None, [c_vp, c_int]),
             "vxo_position": (c_int, [c_vp]),
             "vxo_set_position": (None, [c_vp, c_int]),
             "vxo_buffer": (c_vp, [c_vp, ctypes.c_char_p, ctypes.POINTER(c_int)]),
@@ -270,6 +271,10 @@ class OracleEngine:
 
     def reset(self):
         lib().vxo_reset(self._h)
+
+    def set_kv_f16(self, on=True):
+        """Store new K/V rows rounded to f16 (the engine's KV precision)."""
+        lib().vxo_set_kv_f16(self._h, int(bool(on)))
 
     def buffer(self, name):
         n = c_int(0)

@@ -512,6 +512,7 @@ struct vxo_engine {
   /* batched dataflow scratch */
   float *time_proj_table; /* [nfe-1][dim] */
   int time_table_ready;
+  int kv_f16; /* store K/V rows rounded to f16 (the BASELINE KV precision) */
 };
 
 void vxo_default_config(vxo_config *c) {
@@ -721,6 +722,7 @@ int vxo_is_ready(const vxo_engine *e) {
 }
 
 void vxo_reset(vxo_engine *e) { e->position = 0; }
+void vxo_set_kv_f16(vxo_engine *e, int on) { e->kv_f16 = on; }
 int vxo_position(const vxo_engine *e) { return e->position; }
 void vxo_set_position(vxo_engine *e, int pos) { e->position = pos; }
 float *vxo_kv(vxo_engine *e, int layer, int which) {
@@ -812,6 +814,13 @@ void vxo_backbone_step_ex(vxo_engine *e, int token, int mode,
     vxo_rope(e->k, c->head_dim, pos, c->n_kv_heads, c->rope_theta);
     memcpy(e->kv_k[l] + (size_t)pos * kvd, e->k, (size_t)kvd * sizeof(float));
     memcpy(e->kv_v[l] + (size_t)pos * kvd, e->v, (size_t)kvd * sizeof(float));
+    if (e->kv_f16) { /* f16 KV storage: the cached row is the f16 rounding */
+      float *kr = e->kv_k[l] + (size_t)pos * kvd, *vr = e->kv_v[l] + (size_t)pos * kvd;
+      for (int i = 0; i < kvd; i++) {
+        kr[i] = vxo_f16_to_f32(vxo_f32_to_f16(kr[i]));
+        vr[i] = vxo_f16_to_f32(vxo_f32_to_f16(vr[i]));
+      }
+    }
     int seq = pos + 1;
     vxo_attn_scores(e->q, e->kv_k[l], e->scores, c->n_heads, c->n_kv_heads,
                     c->head_dim, seq);

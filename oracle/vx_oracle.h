@@ -100,6 +100,9 @@ const uint16_t *vxo_weight(const vxo_engine *e, const char *name);
 int vxo_is_ready(const vxo_engine *e);
 
 void vxo_reset(vxo_engine *e);
+/* on != 0: new K/V rows are stored rounded to f16 (the reference keeps
+ * f32; the HIP engine keeps f16 as the benchmark configurations specify). */
+void vxo_set_kv_f16(vxo_engine *e, int on);
 int vxo_position(const vxo_engine *e);
 void vxo_set_position(vxo_engine *e, int pos);
 float *vxo_buffer(vxo_engine *e, const char *name, int *count);

@@ -75,7 +75,9 @@ struct vx_engine {
   bool tproj_ready = false;
 
   int host_pos = 0;
-  hipGraphExec_t step_exec = nullptr, hold_exec = nullptr, frame_exec = nullptr;
+  hipGraphExec_t step_exec = nullptr, hold_exec = nullptr, frame_exec = nullptr,
+                 fm_greedy_exec = nullptr, fm_plain_exec = nullptr;
+  bool use_graphs = true;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
 
   uint16_t *kc(int l) const { return kv + (size_t)(2 * l) * NKV * max_seq * HD; }
@@ -148,13 +150,26 @@ GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, in
 
 }  // namespace
 
-// One backbone layer: 5 launches (QKV+rope+KV write | attention | O +
-// residual | norm + gate/up + SwiGLU | down + residual).
+// Streaming GEMV launch: M units split exactly into blocks of WAVES*UPW.
+template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K>
+void launch_gemv1(hipStream_t st, const GemvArgs &a) {
+  constexpr int per_block = WAVES * UPW;
+  hipLaunchKernelGGL((gemv1_kernel<WAVES, UPW, UPG, EPI, NORM, K>), dim3(a.M / per_block),
+                     dim3(WAVES * 64), 0, st, a);
+}
+// unit counts of the backbone GEMVs must split into whole blocks
+static_assert((QKV_ROWS / 2) % (6 * 2) == 0 && DIM % (6 * 2) == 0 && HID % (12 * 3) == 0 &&
+                  DIM % 12 == 0,
+              "launch shapes");
+
+// One backbone layer: 6 launches (norm + QKV + rope + KV write | attention
+// partials | attention combine | O + residual | norm + gate/up + SwiGLU |
+// down + residual).
 static void enqueue_layer(vx_engine *e, int l, int only = -1) {
   const LayerW &W = e->L[l];
   hipStream_t st = e->st;
   if (only < 0 || only == VX_KERNEL_QKV) {
-    GemvArgs a = gargs(W.wqkv, e->x, DIM, e->q, 0, QKV_ROWS);
+    GemvArgs a = gargs(W.wqkv, e->x, DIM, e->q, 0, QKV_ROWS / 2);
     a.norm_w = W.attn_norm;
     a.eps = e->cfg.norm_eps;
     a.pos = e->pos;
@@ -162,26 +177,27 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
     a.vc = e->vc(l);
     a.max_seq = e->max_seq;
     a.theta = e->cfg.rope_theta;
-    launch_gemv<1, W4, 2, EPI_QKV_ROPE, true, DIM, DIM>(st, a);
+    launch_gemv1<6, 2, 1, EPI_QKV_ROPE, true, DIM>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_ATTN) {
-    AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->counter, e->attn};
-    hipLaunchKernelGGL(attn_decode_kernel, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
+    AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn};
+    hipLaunchKernelGGL(attn_partial_kernel, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->attn);
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
     GemvArgs a = gargs(W.wo, e->attn, QD, e->x, 0, DIM);
-    launch_gemv<1, W4, 1, EPI_RESID, false, QD, QD>(st, a);
+    launch_gemv1<6, 2, 1, EPI_RESID, false, QD>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_GATEUP) {
     GemvArgs a = gargs(W.w1, e->x, DIM, e->act, 0, HID);
     a.W2 = W.w3;
     a.norm_w = W.ffn_norm;
     a.eps = e->cfg.norm_eps;
-    launch_gemv<1, W4, 2, EPI_SWIGLU, true, DIM, DIM>(st, a);
+    launch_gemv1<12, 3, 1, EPI_SWIGLU, true, DIM>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_DOWN) {
     GemvArgs a = gargs(W.w2, e->act, HID, e->x, 0, DIM);
-    launch_gemv<1, W4, 1, EPI_RESID, false, HID, HID>(st, a);
+    launch_gemv1<12, 1, 1, EPI_RESID, false, HID>(st, a);
   }
 }
 
@@ -286,21 +302,46 @@ static int capture(vx_engine *e, hipGraphExec_t *out, void (*body)(vx_engine *))
   return VX_OK;
 }
 
-static void frame_body(vx_engine *e) {
-  hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
-                     e->sem_code, e->codes, e->x);
-  enqueue_backbone(e);
+// FM part of a frame: seeded device noise, then fmForward; greedy stores
+// the masked argmax as the device semantic code (no host round trip).
+static void fm_greedy_body(vx_engine *e) {
   hipLaunchKernelGGL(fm_noise_kernel, dim3(1), dim3(64), 0, e->st, e->noise, e->noise_seed,
                      kNoiseStream, e->frame);
   enqueue_fm(e, e->noise, true);
 }
+static void fm_plain_body(vx_engine *e) {
+  hipLaunchKernelGGL(fm_noise_kernel, dim3(1), dim3(64), 0, e->st, e->noise, e->noise_seed,
+                     kNoiseStream, e->frame);
+  enqueue_fm(e, e->noise, false);
+}
+static void frame_body(vx_engine *e) {
+  hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
+                     e->sem_code, e->codes, e->x);
+  enqueue_backbone(e);
+  fm_greedy_body(e);
+}
 
-static int ensure_graphs(vx_engine *e) {
-  if (!e->step_exec) {
-    int rc = capture(e, &e->step_exec, enqueue_backbone);
+// Runs one captured sequence: replays its hipGraph (captured on first use),
+// or, when graphs are off (VX_NO_GRAPH=1, e.g. under a kernel tracer),
+// enqueues the same kernels directly.
+static int run_seq(vx_engine *e, hipGraphExec_t *slot, void (*body)(vx_engine *)) {
+  if (!e->use_graphs) {
+    body(e);
+    LAUNCHCHK(e);
+    return VX_OK;
+  }
+  if (!*slot) {
+    int rc = capture(e, slot, body);
     if (rc) return rc;
   }
+  HIPCHK(e, hipGraphLaunch(*slot, e->st));
   return VX_OK;
+}
+static int run_step(vx_engine *e) {
+  return run_seq(e, &e->step_exec, enqueue_backbone);
+}
+static int run_step_hold(vx_engine *e) {
+  return run_seq(e, &e->hold_exec, enqueue_backbone_hold);
 }
 
 // ---------------------------------------------------------------- helpers
@@ -400,6 +441,10 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
 
   vx_engine *e = new vx_engine();
   e->cfg = cfg;
+  {
+    const char *ng = getenv("VX_NO_GRAPH");
+    e->use_graphs = !(ng && ng[0] && ng[0] != '0');
+  }
   e->max_seq = max_seq;
   if (hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking) != hipSuccess) {
     delete e;
@@ -537,6 +582,7 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
     vx_destroy(e);
     return fail(nullptr, VX_E_DEVICE, "device initialisation failed");
   }
+
   *out = e;
   return VX_OK;
 }
@@ -546,6 +592,8 @@ void vx_destroy(vx_engine *e) {
   if (e->st) (void)hipStreamSynchronize(e->st);
   if (e->step_exec) (void)hipGraphExecDestroy(e->step_exec);
   if (e->hold_exec) (void)hipGraphExecDestroy(e->hold_exec);
+  if (e->fm_greedy_exec) (void)hipGraphExecDestroy(e->fm_greedy_exec);
+  if (e->fm_plain_exec) (void)hipGraphExecDestroy(e->fm_plain_exec);
   if (e->frame_exec) (void)hipGraphExecDestroy(e->frame_exec);
   if (e->warena) (void)hipFree(e->warena);
   if (e->kv) (void)hipFree(e->kv);
@@ -591,6 +639,17 @@ int vx_init_synthetic(vx_engine *e, uint64_t seed, float std) {
   return VX_OK;
 }
 
+int vx_read_tensor(vx_engine *e, const char *name, uint16_t *f16, size_t numel) {
+  if (!e || !name || !f16) return e ? fail(e, VX_E_INVALID, "NULL argument") : VX_E_INVALID;
+  auto it = e->slots.find(name);
+  if (it == e->slots.end()) return fail(e, VX_E_INVALID, "Unknown tensor: %s", name);
+  if (numel > it->second.numel)
+    return fail(e, VX_E_INVALID, "%s holds %zu elements", name, it->second.numel);
+  HIPCHK(e, hipMemcpyAsync(f16, it->second.ptr, numel * 2, hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
 int vx_is_ready(const vx_engine *e) {
   if (!e) return 0;
   for (auto &kv : e->slots)
@@ -626,9 +685,8 @@ int vx_backbone_step(vx_engine *e, int32_t token, int32_t mode, const float *pre
   if (!e) return VX_E_INVALID;
   int rc = check_ready(e);
   if (rc) return rc;
-  if ((rc = ensure_graphs(e))) return rc;
   if ((rc = prepare_input(e, token, mode, pre))) return rc;
-  HIPCHK(e, hipGraphLaunch(e->step_exec, e->st));
+  if ((rc = run_step(e))) return rc;
   e->host_pos++;
   if (lm_head) {
     enqueue_lm_head(e);
@@ -882,7 +940,7 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
   HIPCHK(e, hipStreamSynchronize(e->st));
   auto t0 = clk::now();
   if (on_stage) on_stage(user, 0, -1.0);
-  if ((rc = ensure_graphs(e)) || (rc = ensure_tproj(e))) return rc;
+  if ((rc = ensure_tproj(e))) return rc;
   // prefill, one token per step (src/engine.ts:2457-2472); the LM head the
   // reference runs per prefill token is never read, so it is skipped
   for (int i = 0; i < n_tokens; i++) {
@@ -890,7 +948,7 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
     if ((rc = prepare_input(e, tokens[i], is_voice ? VX_EMBED_PRECOMPUTED : VX_EMBED_TOKEN,
                             is_voice ? voice + (size_t)(i - audio_start) * DIM : nullptr)))
       return rc;
-    HIPCHK(e, hipGraphLaunch(e->step_exec, e->st));
+    if ((rc = run_step(e))) return rc;
     e->host_pos++;
   }
   HIPCHK(e, hipStreamSynchronize(e->st));
@@ -901,7 +959,7 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
   }
   // AUDIO token kick (src/engine.ts:2478-2487)
   if ((rc = prepare_input(e, 24, VX_EMBED_TOKEN, nullptr))) return rc;
-  HIPCHK(e, hipGraphLaunch(e->step_exec, e->st));
+  if ((rc = run_step(e))) return rc;
   e->host_pos++;
 
   uint64_t rng = opt.seed ^ 0x5bd1e9955bd1e995ull;
@@ -911,14 +969,13 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
   for (int f = 0; f < max_frames; f++) {
     if (f > 0) {
       if ((rc = prepare_input(e, 0, VX_EMBED_CODES, nullptr))) return rc;
-      HIPCHK(e, hipGraphLaunch(e->step_exec, e->st));
+      if ((rc = run_step(e))) return rc;
       e->host_pos++;
     }
-    hipLaunchKernelGGL(fm_noise_kernel, dim3(1), dim3(64), 0, e->st, e->noise, e->noise_seed,
-                       kNoiseStream, e->frame);
     const bool greedy = opt.sampling == VX_SAMPLE_GREEDY;
-    enqueue_fm(e, e->noise, greedy);
-    LAUNCHCHK(e);
+    rc = greedy ? run_seq(e, &e->fm_greedy_exec, fm_greedy_body)
+                : run_seq(e, &e->fm_plain_exec, fm_plain_body);
+    if (rc) return rc;
     uint32_t code;
     if (greedy) {
       HIPCHK(e, hipMemcpyAsync(&code, e->sem_code, 4, hipMemcpyDeviceToHost, e->st));
@@ -964,11 +1021,11 @@ int vx_time_backbone_steps(vx_engine *e, int32_t n, int32_t hold, float *out_ms)
   int rc = check_ready(e);
   if (rc) return rc;
   if (e->host_pos + (hold ? 1 : n) > e->max_seq) return fail(e, VX_E_RANGE, "steps pass max_seq_len");
-  if ((rc = ensure_graphs(e))) return rc;
-  if (hold && !e->hold_exec && (rc = capture(e, &e->hold_exec, enqueue_backbone_hold))) return rc;
-  hipGraphExec_t g = hold ? e->hold_exec : e->step_exec;
   HIPCHK(e, hipEventRecord(e->ev0, e->st));
-  for (int i = 0; i < n; i++) HIPCHK(e, hipGraphLaunch(g, e->st));
+  for (int i = 0; i < n; i++) {
+    rc = hold ? run_step_hold(e) : run_step(e);
+    if (rc) return rc;
+  }
   HIPCHK(e, hipEventRecord(e->ev1, e->st));
   HIPCHK(e, hipEventSynchronize(e->ev1));
   if (!hold) e->host_pos += n;
@@ -982,9 +1039,12 @@ int vx_time_frames(vx_engine *e, int32_t n, float *out_ms) {
   if (rc) return rc;
   if (e->host_pos + n > e->max_seq) return fail(e, VX_E_RANGE, "frames pass max_seq_len");
   if ((rc = ensure_tproj(e))) return rc;
-  if (!e->frame_exec && (rc = capture(e, &e->frame_exec, frame_body))) return rc;
+  if (e->use_graphs && !e->frame_exec && (rc = capture(e, &e->frame_exec, frame_body)))
+    return rc;
   HIPCHK(e, hipEventRecord(e->ev0, e->st));
-  for (int i = 0; i < n; i++) HIPCHK(e, hipGraphLaunch(e->frame_exec, e->st));
+  for (int i = 0; i < n; i++) {
+    if ((rc = run_seq(e, &e->frame_exec, frame_body))) return rc;
+  }
   HIPCHK(e, hipEventRecord(e->ev1, e->st));
   HIPCHK(e, hipEventSynchronize(e->ev1));
   e->host_pos += n;

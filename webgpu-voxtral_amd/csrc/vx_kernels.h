@@ -59,11 +59,39 @@ __device__ __forceinline__ float h2f(uint16_t b) {
 __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, RNE
 }
+// IEEE binary16 round-to-nearest-even in integer arithmetic, subnormals
+// included (the hardware conversion flushes f16 subnormals); used where
+// results must be bit-identical to the CPU generator.
+__device__ __forceinline__ uint16_t f2h_exact(float f) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, f);
+  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u)
+    return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u | ((ax >> 13) & 0x3ffu) : 0x7c00u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  uint32_t q, rem, half;
+  if (ax < 0x38800000u) {  // result is subnormal (or zero): q * 2^-24
+    if (ax <= 0x33000000u) return (uint16_t)sign;
+    const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+    const int rsh = 126 - (int)(ax >> 23);  // 14..24
+    q = m >> rsh;
+    rem = m & ((1u << rsh) - 1u);
+    half = 1u << (rsh - 1);
+  } else {
+    q = (((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13);
+    rem = ax & 0x1fffu;
+    half = 0x1000u;
+  }
+  if (rem > half || (rem == half && (q & 1u))) q++;
+  return (uint16_t)(sign | q);
+}
 
 // acc += sum_j w[j] * x[j] for 8 halves packed in a u32x4
+// (vector elements are copied to scalars first: __builtin_bit_cast of an
+// ext-vector element expression such as w.y reads element 0)
 __device__ __forceinline__ float dot8(u32x4 w, f32x4 xa, f32x4 xb, float acc) {
-  h2 p0 = __builtin_bit_cast(h2, w.x), p1 = __builtin_bit_cast(h2, w.y),
-     p2 = __builtin_bit_cast(h2, w.z), p3 = __builtin_bit_cast(h2, w.w);
+  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3];
+  h2 p0 = __builtin_bit_cast(h2, w0), p1 = __builtin_bit_cast(h2, w1),
+     p2 = __builtin_bit_cast(h2, w2), p3 = __builtin_bit_cast(h2, w3);
   acc = fmaf((float)p0.x, xa.x, acc);
   acc = fmaf((float)p0.y, xa.y, acc);
   acc = fmaf((float)p1.x, xa.z, acc);
@@ -174,10 +202,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
           rowp = ((r & 1) ? a.W2 : a.W) + (size_t)(unit0 + (r >> 1)) * K;
         else
           rowp = a.W + (size_t)min(unit0 + r, a.M - 1) * K;
+        // plain 16-byte loads: __builtin_nontemporal_load on this vector
+        // type lowers to a single dword load on gfx950
 #pragma unroll
         for (int c = 0; c < NCH; c++)
-          w[r][c] = __builtin_nontemporal_load(
-              (const u32x4 *)(rowp + kt + c * 512 + lane * 8));
+          w[r][c] = *(const u32x4 *)(rowp + kt + c * 512 + lane * 8);
       }
 #pragma unroll
       for (int c = 0; c < NCH; c++)
@@ -263,7 +292,146 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
   }
 }
 
-// --------------------------------------------------------- decode attention
+// ------------------------------------------------- streaming GEMV (batch 1)
+// The backbone GEMVs.  One block per CU (grid = number of CUs); block b owns
+// units [b*WAVES*UPW, (b+1)*WAVES*UPW) and wave w a contiguous run of UPW
+// units, processed in groups of UPG units.  A unit is one output row, or a
+// row pair for EPI_SWIGLU (gate row i, up row i) and EPI_QKV_ROPE (rows 2i,
+// 2i+1).  Weights do not depend on the activations, so every wave issues
+// its first group's 16-byte loads before the block stages the (normalised)
+// input vector into LDS, and loads group g+1 while it computes group g.
+template <int EPI>
+constexpr int rows_per_unit() {
+  return (EPI == EPI_SWIGLU || EPI == EPI_QKV_ROPE) ? 2 : 1;
+}
+
+template <int EPI, int K>
+__device__ __forceinline__ const uint16_t *unit_row(const GemvArgs &a, int unit, int r) {
+  if (EPI == EPI_SWIGLU) return (r ? a.W2 : a.W) + (size_t)unit * K;
+  if (EPI == EPI_QKV_ROPE) return a.W + (size_t)(2 * unit + r) * K;
+  return a.W + (size_t)unit * K;
+}
+
+template <int EPI, int K, int UPG>
+__device__ __forceinline__ void load_group(const GemvArgs &a, int unit0, int lane,
+                                           u32x4 (&w)[UPG * rows_per_unit<EPI>()][K / 512]) {
+  constexpr int RU = rows_per_unit<EPI>();
+#pragma unroll
+  for (int u = 0; u < UPG; u++)
+#pragma unroll
+    for (int r = 0; r < RU; r++) {
+      const uint16_t *p = unit_row<EPI, K>(a, unit0 + u, r) + lane * 8;
+#pragma unroll
+      for (int c = 0; c < K / 512; c++) w[u * RU + r][c] = *(const u32x4 *)(p + c * 512);
+    }
+}
+
+// epilogue of one unit; y[r] = full dot product of the unit's row r
+template <int EPI>
+__device__ __forceinline__ void unit_epilogue(const GemvArgs &a, int unit, const float *y, int pos) {
+  if (EPI == EPI_SWIGLU) {
+    const float g = y[0];
+    a.out[unit] = (g / (1.0f + expf(-g))) * y[1];
+  } else if (EPI == EPI_QKV_ROPE) {
+    const int row = 2 * unit;
+    const float y0 = y[0], y1 = y[1];
+    if (row < QD + KVD) {
+      const int pair = (row & (HD - 1)) >> 1;
+      const float freq = 1.0f / powf(a.theta, (float)(pair * 2) / (float)HD);
+      const float ang = (float)pos * freq;
+      const float cs = cosf(ang), sn = sinf(ang);
+      const float r0 = y0 * cs - y1 * sn, r1 = y0 * sn + y1 * cs;
+      if (row < QD) {
+        a.out[row] = r0;
+        a.out[row + 1] = r1;
+      } else {
+        const int c = row - QD;
+        uint16_t *dst = a.kc + ((size_t)(c >> 7) * a.max_seq + pos) * HD + (c & (HD - 1));
+        dst[0] = f2h(r0);
+        dst[1] = f2h(r1);
+      }
+    } else {
+      const int c = row - QD - KVD;
+      uint16_t *dst = a.vc + ((size_t)(c >> 7) * a.max_seq + pos) * HD + (c & (HD - 1));
+      dst[0] = f2h(y0);
+      dst[1] = f2h(y1);
+    }
+  } else if (EPI == EPI_RESID) {
+    a.out[unit] = y[0] + a.out[unit];
+  } else {
+    a.out[unit] = y[0];
+  }
+}
+
+template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K>
+__global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(GemvArgs a) {
+  static_assert(K % 512 == 0 && UPW % UPG == 0, "shape");
+  constexpr int RU = rows_per_unit<EPI>();
+  constexpr int RG = UPG * RU;  // rows per group
+  constexpr int NCH = K / 512;
+  constexpr int G = UPW / UPG;
+  constexpr int NT = WAVES * 64;
+  __shared__ __attribute__((aligned(16))) float xl[K];
+  __shared__ float red[WAVES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int u0 = (blockIdx.x * WAVES + wave) * UPW;
+
+  u32x4 wbuf[2][RG][NCH];
+  load_group<EPI, K, UPG>(a, u0, lane, wbuf[0]);
+
+  // stage the input vector (RMSNorm'd: x * rms * w) while the loads fly
+  float scale = 1.0f;
+  if (NORM) {
+    float s = 0.f;
+    for (int i = tid * 4; i < K; i += NT * 4) {
+      f32x4 v = *(const f32x4 *)(a.x + i);
+      s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    s = wave_sum(s);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; w++) tot += red[w];
+    scale = 1.0f / sqrtf(tot / (float)K + a.eps);
+  }
+  for (int i = tid * 4; i < K; i += NT * 4) {
+    f32x4 v = *(const f32x4 *)(a.x + i);
+    if (NORM) {
+      const uint16_t *g = a.norm_w + i;
+      v.x = v.x * scale * h2f(g[0]);
+      v.y = v.y * scale * h2f(g[1]);
+      v.z = v.z * scale * h2f(g[2]);
+      v.w = v.w * scale * h2f(g[3]);
+    }
+    *(f32x4 *)(xl + i) = v;
+  }
+  __syncthreads();
+  const int pos = (EPI == EPI_QKV_ROPE) ? *a.pos : 0;
+
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    if (g + 1 < G) load_group<EPI, K, UPG>(a, u0 + (g + 1) * UPG, lane, wbuf[(g + 1) & 1]);
+    float acc[RG];
+#pragma unroll
+    for (int r = 0; r < RG; r++) acc[r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+      const float *xp = xl + c * 512 + lane * 8;
+      const f32x4 xa = *(const f32x4 *)xp, xb = *(const f32x4 *)(xp + 4);
+#pragma unroll
+      for (int r = 0; r < RG; r++) acc[r] = dot8(wbuf[g & 1][r][c], xa, xb, acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < RG; r++) acc[r] = wave_sum(acc[r]);
+    if (lane == 0) {
+#pragma unroll
+      for (int u = 0; u < UPG; u++) unit_epilogue<EPI>(a, u0 + g * UPG + u, acc + u * RU, pos);
+    }
+  }
+}
+
+// --------------------------------------------------- decode attention v2
 struct AttnArgs {
   const float *q;        // [NH*HD], roped
   const uint16_t *kc;    // layer K cache [NKV][max_seq][HD]
@@ -271,16 +439,16 @@ struct AttnArgs {
   const int *pos;        // decode position; keys 0..pos
   int max_seq;
   float *part;           // [NH][ATTN_SPLITS][HD + 2] (o, m, l)
-  int *counter;          // [NKV] arrival counters, zero between launches
   float *out;            // [NH*HD]
 };
 
-// grid (ATTN_SPLITS, NKV), 256 threads: wave w handles query head
-// 4*kv_head + w over this split's key range.  Scores use one lane per key
-// (q broadcast from LDS), values one lane per 2 dims.  The last block of a
-// KV head to finish merges the splits: M = max m_s, L = sum l_s e^(m_s-M),
-// o = sum o_s e^(m_s-M) / L.
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+// Partials: grid (ATTN_SPLITS, NKV), 256 threads, wave w = query head
+// 4*kv_head + w, split s covers keys [s*chunk, min(seq, (s+1)*chunk)),
+// chunk = ceil(seq / ATTN_SPLITS).  Each pass of up to 64 keys issues the
+// K-row loads (one key per lane) and the V loads (2 dims per lane, one row
+// per key) together, then scores, a local softmax and P.V.  No cross-block
+// communication: attn_combine_kernel merges the splits in the next launch.
+__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = kvh * (NH / NKV) + wave;
@@ -289,62 +457,47 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
   const int p0 = split * chunk, p1 = min(seq, p0 + chunk);
   __shared__ __attribute__((aligned(16))) float qs[4][HD];
   __shared__ float ps[4][64];
-  __shared__ int is_last;
   const float scale = 1.0f / sqrtf((float)HD);
+  const uint16_t *Kb = a.kc + (size_t)kvh * a.max_seq * HD;
+  const uint16_t *Vb = a.vc + (size_t)kvh * a.max_seq * HD;
 
   qs[wave][lane * 2] = a.q[h * HD + lane * 2];
   qs[wave][lane * 2 + 1] = a.q[h * HD + lane * 2 + 1];
   __syncthreads();
 
-  const uint16_t *Kb = a.kc + (size_t)kvh * a.max_seq * HD;
-  const uint16_t *Vb = a.vc + (size_t)kvh * a.max_seq * HD;
   float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
   for (int pb = p0; pb < p1; pb += 64) {
-    const int p = pb + lane;
-    float s = -INFINITY;
-    if (p < p1) {
-      const u32x4 *kr = (const u32x4 *)(Kb + (size_t)p * HD);
-      float dot = 0.f;
+    const int n = min(64, p1 - pb);
+    const int p = pb + min(lane, n - 1);  // lanes past n re-read a valid row
+    u32x4 kr[HD / 8];
+    const u32x4 *kp = (const u32x4 *)(Kb + (size_t)p * HD);
 #pragma unroll
-      for (int c = 0; c < HD / 8; c++) {
-        u32x4 kv = kr[c];
-        f32x4 xa = *(const f32x4 *)&qs[wave][c * 8];
-        f32x4 xb = *(const f32x4 *)&qs[wave][c * 8 + 4];
-        dot = dot8(kv, xa, xb, dot);
-      }
-      s = dot * scale;
-    }
+    for (int c = 0; c < HD / 8; c++) kr[c] = kp[c];
+    uint32_t vv[64];
+    const uint16_t *vp = Vb + (size_t)pb * HD + lane * 2;
+#pragma unroll
+    for (int j = 0; j < 64; j++) vv[j] = *(const uint32_t *)(vp + (size_t)min(j, n - 1) * HD);
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < HD / 8; c++)
+      dot = dot8(kr[c], *(const f32x4 *)&qs[wave][c * 8], *(const f32x4 *)&qs[wave][c * 8 + 4], dot);
+    const float s = lane < n ? dot * scale : -INFINITY;
     const float mnew = fmaxf(m, wave_max(s));
-    const float e = (p < p1) ? expf(s - mnew) : 0.f;
+    const float e = lane < n ? expf(s - mnew) : 0.f;
     const float corr = expf(m - mnew);
     l = l * corr + wave_sum(e);
     o0 *= corr;
     o1 *= corr;
     ps[wave][lane] = e;
-    __builtin_amdgcn_wave_barrier();
-    const int n = min(64, p1 - pb);
-    const uint16_t *vp = Vb + (size_t)pb * HD + lane * 2;
-    int j = 0;
-    for (; j + 4 <= n; j += 4) {
-      uint32_t v0 = *(const uint32_t *)(vp + (size_t)(j + 0) * HD);
-      uint32_t v1 = *(const uint32_t *)(vp + (size_t)(j + 1) * HD);
-      uint32_t v2 = *(const uint32_t *)(vp + (size_t)(j + 2) * HD);
-      uint32_t v3 = *(const uint32_t *)(vp + (size_t)(j + 3) * HD);
-      h2 a0 = __builtin_bit_cast(h2, v0), a1 = __builtin_bit_cast(h2, v1),
-         a2 = __builtin_bit_cast(h2, v2), a3 = __builtin_bit_cast(h2, v3);
-      float e0 = ps[wave][j], e1 = ps[wave][j + 1], e2 = ps[wave][j + 2], e3 = ps[wave][j + 3];
-      o0 = fmaf(e0, (float)a0.x, o0); o1 = fmaf(e0, (float)a0.y, o1);
-      o0 = fmaf(e1, (float)a1.x, o0); o1 = fmaf(e1, (float)a1.y, o1);
-      o0 = fmaf(e2, (float)a2.x, o0); o1 = fmaf(e2, (float)a2.y, o1);
-      o0 = fmaf(e3, (float)a3.x, o0); o1 = fmaf(e3, (float)a3.y, o1);
-    }
-    for (; j < n; j++) {
-      h2 v = __builtin_bit_cast(h2, *(const uint32_t *)(vp + (size_t)j * HD));
-      float ej = ps[wave][j];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 64; j++) {
+      const h2 v = __builtin_bit_cast(h2, vv[j]);
+      const float ej = ps[wave][j];  // 0 for j >= n
       o0 = fmaf(ej, (float)v.x, o0);
       o1 = fmaf(ej, (float)v.y, o1);
     }
-    __builtin_amdgcn_wave_barrier();
+    __syncthreads();
     m = mnew;
   }
   float *pp = a.part + ((size_t)h * ATTN_SPLITS + split) * (HD + 2);
@@ -354,32 +507,31 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
     pp[HD] = m;
     pp[HD + 1] = l;
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) is_last = (atomicAdd(&a.counter[kvh], 1) == ATTN_SPLITS - 1);
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  // merge: lane s < ATTN_SPLITS holds split s's (m, l)
-  const float *hp = a.part + (size_t)h * ATTN_SPLITS * (HD + 2);
+}
+
+// Combine: one wave per query head.  M = max m_s, L = sum l_s e^(m_s - M),
+// o = sum o_s e^(m_s - M) / L (splits without keys carry m = -inf, l = 0).
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, float *out) {
+  const int h = blockIdx.x, lane = threadIdx.x;
+  const float *hp = part + (size_t)h * ATTN_SPLITS * (HD + 2);
   float ms = -INFINITY, ls = 0.f;
   if (lane < ATTN_SPLITS) {
-    ms = __builtin_nontemporal_load(hp + lane * (HD + 2) + HD);
-    ls = __builtin_nontemporal_load(hp + lane * (HD + 2) + HD + 1);
+    ms = hp[lane * (HD + 2) + HD];
+    ls = hp[lane * (HD + 2) + HD + 1];
   }
   const float M = wave_max(ms);
   const float wgt = (lane < ATTN_SPLITS) ? expf(ms - M) : 0.f;
   const float L = wave_sum(ls * wgt);
   float r0 = 0.f, r1 = 0.f;
+#pragma unroll 8
   for (int s = 0; s < ATTN_SPLITS; s++) {
-    float ws = __shfl(wgt, s, 64);
+    const float ws = __shfl(wgt, s, 64);
     const float *op = hp + s * (HD + 2) + lane * 2;
-    r0 = fmaf(ws, __builtin_nontemporal_load(op), r0);
-    r1 = fmaf(ws, __builtin_nontemporal_load(op + 1), r1);
+    r0 = fmaf(ws, op[0], r0);
+    r1 = fmaf(ws, op[1], r1);
   }
-  a.out[h * HD + lane * 2] = r0 / L;
-  a.out[h * HD + lane * 2 + 1] = r1 / L;
-  if (tid == 0) a.counter[kvh] = 0;
+  out[h * HD + lane * 2] = r0 / L;
+  out[h * HD + lane * 2 + 1] = r1 / L;
 }
 
 // ------------------------------------------------------- small kernels
@@ -477,7 +629,7 @@ __global__ void gen_f16_kernel(uint16_t *out, size_t n, uint64_t seed, uint64_t 
   size_t stride = (size_t)gridDim.x * blockDim.x;
   for (; i < n; i += stride) {
     float t = __fmul_rn(normal_variate(seed, stream, i), std);
-    out[i] = f2h(__fadd_rn(mean, t));
+    out[i] = f2h_exact(__fadd_rn(mean, t));
   }
 }
 
@@ -490,7 +642,7 @@ __global__ void gen_kv_kernel(uint16_t *cache, int max_seq, int npos, uint64_t s
   size_t stride = (size_t)gridDim.x * blockDim.x;
   for (; i < n; i += stride) {
     int p = (int)(i / KVD), c = (int)(i % KVD);
-    cache[((size_t)(c >> 7) * max_seq + p) * HD + (c & 127)] = f2h(normal_variate(seed, stream, i));
+    cache[((size_t)(c >> 7) * max_seq + p) * HD + (c & 127)] = f2h_exact(normal_variate(seed, stream, i));
   }
 }
 

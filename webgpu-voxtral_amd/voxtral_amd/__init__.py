@@ -69,6 +69,7 @@ _SIGS = {
     "vx_last_error": (ctypes.c_char_p, [_VP]),
     "vx_load_tensor": (_I32, [_VP, ctypes.c_char_p, _VP, ctypes.c_size_t, _VP, _I32]),
     "vx_init_synthetic": (_I32, [_VP, ctypes.c_uint64, ctypes.c_float]),
+    "vx_read_tensor": (_I32, [_VP, ctypes.c_char_p, _VP, ctypes.c_size_t]),
     "vx_is_ready": (_I32, [_VP]),
     "vx_reset": (_I32, [_VP]),
     "vx_position": (_I32, [_VP]),
@@ -192,6 +193,11 @@ class VoxtralEngine:
         """tensors: mapping of reference tensor name -> float16 array."""
         for name, arr in tensors.items():
             self.load_tensor(name, arr)
+
+    def read_tensor(self, name, numel):
+        out = np.empty(int(numel), np.uint16)
+        self._check(self._lib.vx_read_tensor(self._h, name.encode(), out.ctypes.data, out.size))
+        return out
 
     def init_synthetic(self, seed=0, std=0.02):
         self._check(self._lib.vx_init_synthetic(self._h, seed, std))
