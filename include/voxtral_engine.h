@@ -57,6 +57,12 @@ typedef struct vx_config {
   int32_t semantic_vocab;  /* 8320 */
   int32_t acoustic_levels; /* 21 */
   int32_t audio_vocab;     /* 9088 */
+  /* KV cache element type (no reference field): 0 = f32, the reference's
+   * KV precision (src/engine.ts:510-530), the default; 1 = f16, half the KV
+   * traffic.  Rounding cached K/V rows to f16 perturbs hidden states by
+   * more than 1e-2 after 26 random-weight layers, so parity with the
+   * reference holds for 0 only. */
+  int32_t kv_f16;
 } vx_config;
 
 /* defaultConfig, src/types.ts:70-122 */
@@ -144,15 +150,16 @@ int vx_read(vx_engine *e, const char *buffer, float *dst, size_t count);
 int vx_write(vx_engine *e, const char *buffer, const float *src, size_t count);
 
 /* KV cache access (no reference counterpart; test and prefill plumbing).
- * Layout seen by the caller: [pos][n_kv_heads * head_dim] f16 bits, the
- * reference's [maxSeq, 1024] row order (src/engine.ts:510-530). */
+ * Layout seen by the caller: [pos][n_kv_heads * head_dim] f32, the
+ * reference's [maxSeq, 1024] row order (src/engine.ts:510-530).  With an
+ * f16 cache, writes round to nearest even and reads widen exactly. */
 int vx_write_kv(vx_engine *e, int32_t layer, int32_t which /*0=K,1=V*/,
-                int32_t pos0, int32_t npos, const uint16_t *f16);
+                int32_t pos0, int32_t npos, const float *src);
 int vx_read_kv(vx_engine *e, int32_t layer, int32_t which, int32_t pos0,
-               int32_t npos, uint16_t *f16);
-/* Fills positions [0, npos) of every layer's K and V with N(0,1) f16 from
- * the generator (stream "kv.<layer>.k"/"kv.<layer>.v", element index
- * pos*1024 + c). */
+               int32_t npos, float *dst);
+/* Fills positions [0, npos) of every layer's K and V with N(0,1) values
+ * rounded to f16 from the generator (stream "kv.<layer>.k"/"kv.<layer>.v",
+ * element index pos*1024 + c), held exactly in either cache type. */
 int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos);
 
 /* ----------------------------------------------------------- generate() */

@@ -3,9 +3,10 @@ against the CPU oracle on identical seeded inputs.
 
 Tolerance (hidden states, f16 weights with f32 accumulation): max relative
 error <= 1e-2 with denominator floor 1e-2*||e||_inf, and the reference's
-allclose(atol=1e-2, rtol=1e-2).  Intermediate buffers get a tighter bar
-(they differ from the oracle only by summation order, and by the f16
-storage of the new K/V row, which the reference keeps in f32)."""
+allclose(atol=1e-2, rtol=1e-2).  Intermediate buffers get a tighter bar:
+with the default f32 KV cache they differ from the oracle only by
+summation order and the f32 rounding of the rope angle.  The optional f16
+KV cache is checked against the oracle's f16-KV mode."""
 import numpy as np
 import pytest
 
@@ -23,7 +24,6 @@ def pair1():
     print("[pair1] building 1-layer engines", flush=True)
     g = gpu_engine(n_layers=1, max_seq=1024)
     o = oracle_engine(n_layers=1, max_seq=1024)
-    o.set_kv_f16(True)  # same KV precision as the engine
     yield g, o
     g.destroy()
     o.close()
@@ -33,11 +33,15 @@ def test_kv_generator_bit_identical(pair1):
     g, o = pair1
     g.fill_kv_synthetic(SEED, 128)
     got = g.read_kv(0, 0, 0, 128)
-    ref = O.gen_f16(SEED, "kv.0.k", 128 * 1024).reshape(128, 1024)
-    assert np.array_equal(got, ref)
+    ref = O.f16_bits_to_f32(O.gen_f16(SEED, "kv.0.k", 128 * 1024)).reshape(128, 1024)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
     got = g.read_kv(0, 1, 100, 28)
-    ref = O.gen_f16(SEED, "kv.0.v", 128 * 1024).reshape(128, 1024)[100:]
-    assert np.array_equal(got, ref)
+    ref = O.f16_bits_to_f32(O.gen_f16(SEED, "kv.0.v", 128 * 1024)).reshape(128, 1024)[100:]
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # write/read round trip of arbitrary f32 rows
+    rows = O.gen_f32(SEED + 5, "kv.rows", 3 * 1024).reshape(3, 1024)
+    g.write_kv(0, 1, 500, rows)
+    assert np.array_equal(g.read_kv(0, 1, 500, 3), rows)
 
 
 @pytest.mark.parametrize("name", ["layers.0.attention.wq.weight", "layers.0.attention.wv.weight",
@@ -83,14 +87,14 @@ def test_single_layer_decode_at_128(pair1):
     s_err = max_rel_err(g.debug_read("gate", 9216), o.buffer("gate"))
     print(f"q {q_err:.2e} attn {a_err:.2e} swiglu {s_err:.2e}")
     # q differs from the oracle by the f32 rounding of the rope angle
-    # pos*freq (~|q| * pos * 2^-24 absolute); attention adds the f16 storage
-    # of the new K/V row.  Real defects show errors of order 1.
-    assert q_err < 1e-3 and a_err < 1e-2 and s_err < 1e-3
-    # the new K/V row: f16 of the oracle's f32 row
-    k_new = O.f16_bits_to_f32(g.read_kv(0, 0, 128, 1)[0])
-    np.testing.assert_allclose(k_new, o.kv(0, 0)[128], rtol=1e-3, atol=1e-3 * np.abs(o.kv(0, 0)[128]).max())
-    v_new = O.f16_bits_to_f32(g.read_kv(0, 1, 128, 1)[0])
-    np.testing.assert_allclose(v_new, o.kv(0, 1)[128], rtol=1e-3, atol=1e-3 * np.abs(o.kv(0, 1)[128]).max())
+    # pos*freq (~|q| * pos * 2^-24 absolute) and summation order.  Real
+    # defects show errors of order 1.
+    assert q_err < 1e-3 and a_err < 1e-3 and s_err < 1e-3
+    # the new K/V row (rope'd k, v) in the f32 cache
+    for w in (0, 1):
+        new = g.read_kv(0, w, 128, 1)[0]
+        ref = o.kv(0, w)[128]
+        np.testing.assert_allclose(new, ref, rtol=1e-3, atol=1e-4 * np.abs(ref).max())
     # hidden states at the reference read points
     for k, name in ((0, "attn_out"), (1, "ffn_out")):
         err = max_rel_err(res["layers"][0][name], lo[0, k])
@@ -101,27 +105,21 @@ def test_single_layer_decode_at_128(pair1):
     assert err < 2e-3 and ref_allclose(res["final_norm"], o.buffer("normed"))
 
 
-@pytest.mark.parametrize("pos", [16, 128, 512])
+@pytest.mark.parametrize("pos", [1, 16, 128, 512])
 def test_against_reference_f32_kv(pair1, pos):
-    """Against the reference's own KV precision (f32 cache): the spec bar,
-    max relative error <= 1e-2 and allclose(1e-2, 1e-2).  With a single
-    key the f16 storage of that key's V row alone reaches ~2e-2, so the
-    bar is applied from 16 cached keys up."""
+    """The spec bar against the oracle: max relative error <= 1e-2 and
+    allclose(1e-2, 1e-2)."""
     g, o = pair1
     x = O.gen_f32(SEED + 7, "input.hidden", 3072)
     g.fill_kv_synthetic(SEED, pos)
     fill_oracle_kv(o, SEED, pos)
     g.position = pos
     o.position = pos
-    o.set_kv_f16(False)
-    try:
-        _, gn = g.backbone_step(precomputed=x)
-        o.backbone_step(precomputed=x)
-    finally:
-        o.set_kv_f16(True)
+    _, gn = g.backbone_step(precomputed=x)
+    o.backbone_step(precomputed=x)
     err = max_rel_err(gn, o.buffer("normed"))
-    print(f"pos {pos}: vs f32-KV reference {err:.2e}")
-    assert err < 1e-2 and ref_allclose(gn, o.buffer("normed"))
+    print(f"pos {pos}: vs oracle {err:.2e}")
+    assert err < 1e-3 and ref_allclose(gn, o.buffer("normed"))
 
 
 def test_step_matches_per_layer_path(pair1):
@@ -176,8 +174,8 @@ def test_attention_positions(pair1, pos):
     _, normed = g.backbone_step(precomputed=x)
     o.backbone_step(precomputed=x)
     a_err = max_rel_err(g.debug_read("attn_out", 4096), o.buffer("attn_out"))
-    assert a_err < 1e-2, a_err
-    assert max_rel_err(normed, o.buffer("normed")) < 2e-3
+    assert a_err < 1e-3, a_err
+    assert max_rel_err(normed, o.buffer("normed")) < 1e-3
 
 
 def test_lm_head_argmax(pair1):
@@ -212,7 +210,6 @@ def pair26():
     print("[pair26] building 26-layer engines", flush=True)
     g = gpu_engine(n_layers=26, max_seq=1024)
     o = oracle_engine(n_layers=26, max_seq=1024)
-    o.set_kv_f16(True)
     yield g, o
     g.destroy()
     o.close()
@@ -234,8 +231,6 @@ def test_full_backbone_decode_at_512(pair26):
     assert max_rel_err(g.debug_read("hidden", 3072), o.buffer("hidden")) < 1e-2
 
 
-@pytest.mark.xfail(reason="f16 KV storage: a one-ulp f16 rounding difference of a cached row is "
-                   "amplified ~200x through 26 random-weight layers", strict=False)
 def test_full_backbone_real_prefill(pair26):
     """Prompt tokens through all 26 layers from position 0 (real KV)."""
     g, o = pair26
@@ -247,6 +242,45 @@ def test_full_backbone_real_prefill(pair26):
         o.backbone_step(t)
         err = max_rel_err(gn, o.buffer("normed"))
         assert err < 1e-2, (t, err)
-    kv_g = O.f16_bits_to_f32(g.read_kv(25, 0, 0, len(toks)))
+    kv_g = g.read_kv(25, 0, 0, len(toks))
     kv_o = o.kv(25, 0)[:len(toks)]
     assert max_rel_err(kv_g, kv_o) < 1e-2
+
+
+# ------------------------------------------------------- f16 KV cache option
+@pytest.fixture(scope="module")
+def pair1_f16():
+    print("[pair1_f16] building 1-layer engines, f16 KV", flush=True)
+    g = gpu_engine(n_layers=1, max_seq=1024, kv_f16=True)
+    o = oracle_engine(n_layers=1, max_seq=1024)
+    o.set_kv_f16(True)  # the oracle rounds new K/V rows to f16 as the engine stores them
+    yield g, o
+    g.destroy()
+    o.close()
+
+
+@pytest.mark.parametrize("pos", [0, 1, 65, 128, 1023])
+def test_f16_kv_cache(pair1_f16, pos):
+    """f16 cache: same arithmetic as the oracle's f16-KV mode; the new row
+    is the f16 rounding of the oracle's f32 row."""
+    g, o = pair1_f16
+    x = O.gen_f32(SEED + 11 + pos, "input.hidden", 3072)
+    g.fill_kv_synthetic(SEED, pos)
+    fill_oracle_kv(o, SEED, pos)
+    if pos:
+        assert np.array_equal(g.read_kv(0, 0, 0, pos), o.kv(0, 0)[:pos])
+    g.position = pos
+    o.position = pos
+    _, gn = g.backbone_step(precomputed=x)
+    o.backbone_step(precomputed=x)
+    # a K/V element whose f32 value sits near an f16 rounding boundary can
+    # round the other way (one f16 ulp, 2^-11 relative)
+    a_err = max_rel_err(g.debug_read("attn_out", 4096), o.buffer("attn_out"))
+    assert a_err < 1e-2, a_err
+    assert max_rel_err(gn, o.buffer("normed")) < 2e-3
+    for w in (0, 1):
+        new, ref = g.read_kv(0, w, pos, 1)[0], o.kv(0, w)[pos]
+        np.testing.assert_allclose(new, ref, rtol=2e-3, atol=1e-3 * np.abs(ref).max())
+    rows = O.gen_f32(SEED + 5, "kv.rows", 2 * 1024).reshape(2, 1024)
+    g.write_kv(0, 1, 1000, rows)
+    assert np.array_equal(g.read_kv(0, 1, 1000, 2), rows.astype(np.float16).astype(np.float32))

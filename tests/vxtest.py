@@ -32,9 +32,9 @@ def oracle_engine(n_layers=1, fm_layers=3, max_seq=1024, seed=SEED, std=STD):
     return e
 
 
-def gpu_engine(n_layers=1, fm_layers=3, max_seq=1024, seed=SEED, std=STD):
+def gpu_engine(n_layers=1, fm_layers=3, max_seq=1024, seed=SEED, std=STD, kv_f16=False):
     import voxtral_amd as V
-    cfg = V.default_config(n_layers=n_layers, fm_layers=fm_layers)
+    cfg = V.default_config(n_layers=n_layers, fm_layers=fm_layers, kv_f16=int(kv_f16))
     g = V.VoxtralEngine(cfg, max_seq_len=max_seq).init()
     g.init_synthetic(seed, std)
     return g

@@ -59,8 +59,10 @@ struct vx_engine {
            *fm_sem = nullptr, *fm_ac = nullptr;
   std::map<std::string, Slot> slots;
 
-  // KV cache [layer][K|V][NKV][max_seq][HD]
-  uint16_t *kv = nullptr;
+  // KV cache [layer][K|V][NKV][max_seq][HD], f32 (default) or f16 elements
+  void *kv = nullptr;
+  int kv_f32 = 1;
+  size_t kv_elem = 4;
 
   // activations
   void *aarena = nullptr;
@@ -80,8 +82,8 @@ struct vx_engine {
   bool use_graphs = true;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
 
-  uint16_t *kc(int l) const { return kv + (size_t)(2 * l) * NKV * max_seq * HD; }
-  uint16_t *vc(int l) const { return kv + (size_t)(2 * l + 1) * NKV * max_seq * HD; }
+  void *kc(int l) const { return (char *)kv + (size_t)(2 * l) * NKV * max_seq * HD * kv_elem; }
+  void *vc(int l) const { return (char *)kv + (size_t)(2 * l + 1) * NKV * max_seq * HD * kv_elem; }
   int nsteps() const { return cfg.nfe - 1; }
 };
 
@@ -175,13 +177,17 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
     a.pos = e->pos;
     a.kc = e->kc(l);
     a.vc = e->vc(l);
+    a.kv_f32 = e->kv_f32;
     a.max_seq = e->max_seq;
     a.theta = e->cfg.rope_theta;
     launch_gemv1<6, 2, 1, EPI_QKV_ROPE, true, DIM>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_ATTN) {
     AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn};
-    hipLaunchKernelGGL(attn_partial_kernel, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
+    if (e->kv_f32)
+      hipLaunchKernelGGL(attn_partial_kernel<float>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->attn);
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
@@ -406,6 +412,7 @@ int vx_config_default(vx_config *c) {
   c->semantic_vocab = 8320;
   c->acoustic_levels = 21;
   c->audio_vocab = 9088;
+  c->kv_f16 = 0;
   return VX_OK;
 }
 
@@ -431,7 +438,7 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
                 "FFN 9216, 36 acoustic dims, semantic vocab 8320");
   if (cfg.n_layers < 1 || cfg.n_layers > 64 || cfg.fm_layers < 1 || cfg.fm_layers > 16 ||
       cfg.nfe < 2 || cfg.nfe > 64 || cfg.vocab_size < 25 || cfg.audio_vocab < 9022 ||
-      cfg.acoustic_levels < 2)
+      cfg.acoustic_levels < 2 || (cfg.kv_f16 != 0 && cfg.kv_f16 != 1))
     return fail(nullptr, VX_E_INVALID, "config out of range");
   if (max_seq < 1 || max_seq > (1 << 20))
     return fail(nullptr, VX_E_INVALID, "max_seq_len %d out of range", max_seq);
@@ -446,6 +453,8 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
     e->use_graphs = !(ng && ng[0] && ng[0] != '0');
   }
   e->max_seq = max_seq;
+  e->kv_f32 = cfg.kv_f16 ? 0 : 1;
+  e->kv_elem = cfg.kv_f16 ? 2 : 4;
   if (hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking) != hipSuccess) {
     delete e;
     return fail(nullptr, VX_E_DEVICE, "hipStreamCreate failed");
@@ -529,7 +538,7 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   add_slot(e, "acoustic_transformer.acoustic_codebook_output.weight", e->fm_ac, {NAC, DIM}, false);
 
   // ---- KV cache
-  size_t kvbytes = (size_t)nl * 2 * NKV * max_seq * HD * 2;
+  size_t kvbytes = (size_t)nl * 2 * NKV * max_seq * HD * e->kv_elem;
   if (hipMalloc(&e->kv, kvbytes) != hipSuccess) {
     vx_destroy(e);
     return fail(nullptr, VX_E_NOMEM, "hipMalloc of %zu KV bytes failed", kvbytes);
@@ -821,33 +830,76 @@ int vx_write(vx_engine *e, const char *name, const float *src, size_t count) {
   return VX_OK;
 }
 
+static uint16_t host_f2h(float f) {  // IEEE round-to-nearest-even
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  uint32_t q, rem, half;
+  if (ax < 0x38800000u) {
+    if (ax <= 0x33000000u) return (uint16_t)sign;
+    const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+    const int rsh = 126 - (int)(ax >> 23);
+    q = m >> rsh;
+    rem = m & ((1u << rsh) - 1u);
+    half = 1u << (rsh - 1);
+  } else {
+    q = (((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13);
+    rem = ax & 0x1fffu;
+    half = 0x1000u;
+  }
+  if (rem > half || (rem == half && (q & 1u))) q++;
+  return (uint16_t)(sign | q);
+}
+static float host_h2f(uint16_t h) {
+  const uint32_t e = (h >> 10) & 31u, m = h & 0x3ffu;
+  float v = e == 0 ? (float)m * 0x1p-24f
+                   : e == 31 ? (m ? NAN : INFINITY) : std::ldexp((float)(m | 0x400u), (int)e - 25);
+  return (h & 0x8000u) ? -v : v;
+}
+
+// caller layout [pos][kvh*128 + d] (f32) <-> device [kvh][pos][d] (f32 or f16)
 static int kv_io(vx_engine *e, int32_t layer, int32_t which, int32_t pos0, int32_t npos,
-                 uint16_t *host, bool write) {
+                 float *host, bool write) {
   if (!e || !host) return VX_E_INVALID;
   if (layer < 0 || layer >= e->cfg.n_layers || which < 0 || which > 1 || pos0 < 0 || npos < 0 ||
       pos0 + npos > e->max_seq)
     return fail(e, VX_E_INVALID, "KV range out of bounds");
-  uint16_t *base = which ? e->vc(layer) : e->kc(layer);
-  // caller layout [pos][kvh*128 + d] <-> device [kvh][pos][d]: one 2D copy per head
-  for (int h = 0; h < NKV; h++) {
-    uint16_t *dev = base + ((size_t)h * e->max_seq + pos0) * HD;
-    uint16_t *hp = host + h * HD;
+  if (npos == 0) return VX_OK;
+  char *base = (char *)(which ? e->vc(layer) : e->kc(layer));
+  const size_t es = e->kv_elem, n = (size_t)npos * KVD;
+  std::vector<uint16_t> h16;
+  void *hbuf = host;
+  if (!e->kv_f32) {
+    h16.resize(n);
+    hbuf = h16.data();
     if (write)
-      HIPCHK(e, hipMemcpy2DAsync(dev, HD * 2, hp, KVD * 2, HD * 2, npos, hipMemcpyHostToDevice, e->st));
+      for (size_t i = 0; i < n; i++) h16[i] = host_f2h(host[i]);
+  }
+  for (int h = 0; h < NKV; h++) {
+    char *dev = base + ((size_t)h * e->max_seq + pos0) * HD * es;
+    char *hp = (char *)hbuf + (size_t)h * HD * es;
+    if (write)
+      HIPCHK(e, hipMemcpy2DAsync(dev, HD * es, hp, KVD * es, HD * es, npos, hipMemcpyHostToDevice,
+                                 e->st));
     else
-      HIPCHK(e, hipMemcpy2DAsync(hp, KVD * 2, dev, HD * 2, HD * 2, npos, hipMemcpyDeviceToHost, e->st));
+      HIPCHK(e, hipMemcpy2DAsync(hp, KVD * es, dev, HD * es, HD * es, npos, hipMemcpyDeviceToHost,
+                                 e->st));
   }
   HIPCHK(e, hipStreamSynchronize(e->st));
+  if (!e->kv_f32 && !write)
+    for (size_t i = 0; i < n; i++) host[i] = host_h2f(h16[i]);
   return VX_OK;
 }
 
 int vx_write_kv(vx_engine *e, int32_t layer, int32_t which, int32_t pos0, int32_t npos,
-                const uint16_t *f16) {
-  return kv_io(e, layer, which, pos0, npos, const_cast<uint16_t *>(f16), true);
+                const float *src) {
+  return kv_io(e, layer, which, pos0, npos, const_cast<float *>(src), true);
 }
 
-int vx_read_kv(vx_engine *e, int32_t layer, int32_t which, int32_t pos0, int32_t npos, uint16_t *f16) {
-  return kv_io(e, layer, which, pos0, npos, f16, false);
+int vx_read_kv(vx_engine *e, int32_t layer, int32_t which, int32_t pos0, int32_t npos, float *dst) {
+  return kv_io(e, layer, which, pos0, npos, dst, false);
 }
 
 int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos) {
@@ -856,8 +908,13 @@ int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos) {
   for (int l = 0; l < e->cfg.n_layers; l++)
     for (int w = 0; w < 2; w++) {
       std::string nm = "kv." + std::to_string(l) + (w ? ".v" : ".k");
-      hipLaunchKernelGGL(gen_kv_kernel, dim3(1024), dim3(256), 0, e->st, w ? e->vc(l) : e->kc(l),
-                         e->max_seq, npos, seed, fnv1a(nm.c_str()));
+      void *c = w ? e->vc(l) : e->kc(l);
+      if (e->kv_f32)
+        hipLaunchKernelGGL(gen_kv_kernel<float>, dim3(1024), dim3(256), 0, e->st, (float *)c,
+                           e->max_seq, npos, seed, fnv1a(nm.c_str()));
+      else
+        hipLaunchKernelGGL(gen_kv_kernel<uint16_t>, dim3(1024), dim3(256), 0, e->st, (uint16_t *)c,
+                           e->max_seq, npos, seed, fnv1a(nm.c_str()));
     }
   LAUNCHCHK(e);
   HIPCHK(e, hipStreamSynchronize(e->st));
@@ -1060,8 +1117,8 @@ int vx_time_kernel(vx_engine *e, int32_t kernel, int32_t iters, float *avg_us, d
     return fail(e, VX_E_RANGE, "position %d reaches max_seq_len %d", e->host_pos, e->max_seq);
   const double seq = (double)e->host_pos + 1.0;
   const double b[] = {
-      (double)QKV_ROWS * DIM * 2 + DIM * 2 + DIM * 4 + QD * 4 + 2 * KVD * 2,
-      seq * KVD * 2 * 2 + QD * 4 * 2,
+      (double)QKV_ROWS * DIM * 2 + DIM * 2 + DIM * 4 + QD * 4 + 2.0 * KVD * e->kv_elem,
+      seq * KVD * 2 * (double)e->kv_elem + QD * 4 * 2,
       (double)DIM * QD * 2 + QD * 4 + DIM * 8,
       2.0 * HID * DIM * 2 + DIM * 2 + DIM * 4 + HID * 4,
       (double)DIM * HID * 2 + HID * 4 + DIM * 8,

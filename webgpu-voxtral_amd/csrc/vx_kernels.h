@@ -125,19 +125,36 @@ struct GemvArgs {
   int M;                 // rows (EPI_SWIGLU: row pairs)
   // EPI_QKV_ROPE
   const int *pos;
-  uint16_t *kc, *vc;  // this layer's K and V cache [NKV][max_seq][HD]
+  void *kc, *vc;  // this layer's K and V cache [NKV][max_seq][HD], f32 or f16
+  int kv_f32;     // 1: f32 cache elements (the reference's), 0: f16
   int max_seq;
   float theta;
 };
 
-// Rows handled per wave = RPW (EPI_SWIGLU: RPW/2 pairs).  The block stages
+// one K/V cache element pair (d, d+1) of head row `row` at position pos
+__device__ __forceinline__ void kv_store2(void *cache, int kv_f32, int max_seq, int c, int pos,
+                                          float v0, float v1) {
+  const size_t off = ((size_t)(c >> 7) * max_seq + pos) * HD + (c & (HD - 1));
+  if (kv_f32) {
+    float *d = (float *)cache + off;
+    d[0] = v0;
+    d[1] = v1;
+  } else {
+    uint16_t *d = (uint16_t *)cache + off;
+    d[0] = f2h(v0);
+    d[1] = f2h(v1);
+  }
+}
+
+// Batched GEMV (the FM's CFG batch and the small projections; EPI_QKV_ROPE
+// is served by gemv1_kernel).  Rows handled per wave = RPW (EPI_SWIGLU: RPW/2 pairs).  The block stages
 // the NB input vectors (RMS-normalised when NORM) into LDS one K-tile of KT
 // floats at a time; each lane streams 16-byte weight chunks, chunk c of a
 // row covering columns [c*512 + lane*8, +8), so a wave reads 1 KB of one
 // row per load instruction.
 template <int NB, int WAVES, int RPW, int EPI, bool NORM, int K, int KT>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
-  static_assert(K % KT == 0 && KT % 512 == 0, "tile");
+  static_assert(K % KT == 0 && KT % 512 == 0 && EPI != EPI_QKV_ROPE, "tile");
   constexpr int NT = WAVES * 64;
   constexpr int NCH = KT / 512;
   __shared__ __attribute__((aligned(16))) float xl[NB * KT];
@@ -238,34 +255,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         a.out[(size_t)b * a.os + i] = silu * u;
       }
     }
-  } else if (EPI == EPI_QKV_ROPE) {
-    const int pos = *a.pos;
-#pragma unroll
-    for (int r = 0; r < RPW; r += 2) {
-      const int row = unit0 + r;  // even
-      float y0 = acc[r][0], y1 = acc[r + 1][0];
-      if (row < QD + KVD) {  // q or k: interleaved rope on (row, row+1)
-        int pair = (row & (HD - 1)) >> 1;
-        float freq = 1.0f / powf(a.theta, (float)(pair * 2) / (float)HD);
-        float ang = (float)pos * freq;
-        float cs = cosf(ang), sn = sinf(ang);
-        float r0 = y0 * cs - y1 * sn, r1 = y0 * sn + y1 * cs;
-        if (row < QD) {
-          a.out[row] = r0;
-          a.out[row + 1] = r1;
-        } else {
-          int c = row - QD, kvh = c >> 7, d = c & (HD - 1);
-          uint16_t *dst = a.kc + ((size_t)kvh * a.max_seq + pos) * HD + d;
-          dst[0] = f2h(r0);
-          dst[1] = f2h(r1);
-        }
-      } else {
-        int c = row - QD - KVD, kvh = c >> 7, d = c & (HD - 1);
-        uint16_t *dst = a.vc + ((size_t)kvh * a.max_seq + pos) * HD + d;
-        dst[0] = f2h(y0);
-        dst[1] = f2h(y1);
-      }
-    }
   } else {
 #pragma unroll
     for (int r = 0; r < RPW; r++) {
@@ -345,16 +334,10 @@ __device__ __forceinline__ void unit_epilogue(const GemvArgs &a, int unit, const
         a.out[row] = r0;
         a.out[row + 1] = r1;
       } else {
-        const int c = row - QD;
-        uint16_t *dst = a.kc + ((size_t)(c >> 7) * a.max_seq + pos) * HD + (c & (HD - 1));
-        dst[0] = f2h(r0);
-        dst[1] = f2h(r1);
+        kv_store2(a.kc, a.kv_f32, a.max_seq, row - QD, pos, r0, r1);
       }
     } else {
-      const int c = row - QD - KVD;
-      uint16_t *dst = a.vc + ((size_t)(c >> 7) * a.max_seq + pos) * HD + (c & (HD - 1));
-      dst[0] = f2h(y0);
-      dst[1] = f2h(y1);
+      kv_store2(a.vc, a.kv_f32, a.max_seq, row - QD - KVD, pos, y0, y1);
     }
   } else if (EPI == EPI_RESID) {
     a.out[unit] = y[0] + a.out[unit];
@@ -431,24 +414,72 @@ __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(GemvArgs a) {
   }
 }
 
-// --------------------------------------------------- decode attention v2
+// ------------------------------------------------------ decode attention
 struct AttnArgs {
-  const float *q;        // [NH*HD], roped
-  const uint16_t *kc;    // layer K cache [NKV][max_seq][HD]
-  const uint16_t *vc;
-  const int *pos;        // decode position; keys 0..pos
+  const float *q;   // [NH*HD], roped
+  const void *kc;   // this layer's K cache [NKV][max_seq][HD] (f32 or f16)
+  const void *vc;
+  const int *pos;   // decode position; keys 0..pos
   int max_seq;
-  float *part;           // [NH][ATTN_SPLITS][HD + 2] (o, m, l)
-  float *out;            // [NH*HD]
+  float *part;      // [NH][ATTN_SPLITS][HD + 2] (o, m, l)
+  float *out;       // [NH*HD]
 };
 
-// Partials: grid (ATTN_SPLITS, NKV), 256 threads, wave w = query head
-// 4*kv_head + w, split s covers keys [s*chunk, min(seq, (s+1)*chunk)),
-// chunk = ceil(seq / ATTN_SPLITS).  Each pass of up to 64 keys issues the
-// K-row loads (one key per lane) and the V loads (2 dims per lane, one row
-// per key) together, then scores, a local softmax and P.V.  No cross-block
-// communication: attn_combine_kernel merges the splits in the next launch.
+constexpr int AT_T = 32;  // keys per LDS tile
+
+// Geometry of one K or V tile of AT_T rows staged through LDS: 16-byte
+// chunks, CPT per thread (256 threads), rows padded by 16 bytes so that the
+// 32 lanes reading 32 different K rows at one column spread over the banks.
+template <typename KVT>
+struct KvTile {
+  static constexpr int EPC = 16 / (int)sizeof(KVT);  // elements per chunk
+  static constexpr int CPR = HD / EPC;                // chunks per row
+  static constexpr int CPT = AT_T * CPR / 256;        // chunks per thread
+  static constexpr int LDW = HD + EPC;                // LDS row stride (elements)
+};
+
+template <typename KVT>
+__device__ __forceinline__ void attn_load_tile(const KVT *Kb, const KVT *Vb, int pb, int n, int tid,
+                                               u32x4 (&kr)[KvTile<KVT>::CPT],
+                                               u32x4 (&vr)[KvTile<KVT>::CPT]) {
+  using G = KvTile<KVT>;
+#pragma unroll
+  for (int i = 0; i < G::CPT; i++) {
+    const int id = tid + 256 * i, row = id / G::CPR, col = id % G::CPR;
+    const size_t off = (size_t)(pb + min(row, n - 1)) * HD + col * G::EPC;  // rows past n re-read row n-1
+    kr[i] = *(const u32x4 *)(Kb + off);
+    vr[i] = *(const u32x4 *)(Vb + off);
+  }
+}
+
+// sum over 16 bytes of K elements times 16/sizeof(KVT) query values
+__device__ __forceinline__ float kdot(const float *k, const float *q, float acc) {
+  const f32x4 kv = *(const f32x4 *)k, qv = *(const f32x4 *)q;
+  acc = fmaf(kv.x, qv.x, acc);
+  acc = fmaf(kv.y, qv.y, acc);
+  acc = fmaf(kv.z, qv.z, acc);
+  return fmaf(kv.w, qv.w, acc);
+}
+__device__ __forceinline__ float kdot(const uint16_t *k, const float *q, float acc) {
+  return dot8(*(const u32x4 *)k, *(const f32x4 *)q, *(const f32x4 *)(q + 4), acc);
+}
+__device__ __forceinline__ float2 vpair(const float *v) { return *(const float2 *)v; }
+__device__ __forceinline__ float2 vpair(const uint16_t *v) {
+  const h2 p = __builtin_bit_cast(h2, *(const uint32_t *)v);
+  return make_float2((float)p.x, (float)p.y);
+}
+
+// Partials (attnScore + softmax + attnValue, src/shaders.ts:306-447, split
+// over the key axis): grid (ATTN_SPLITS, NKV), 256 threads, wave w = query
+// head 4*kv_head + w, so the four heads sharing a KV head share every staged
+// tile.  Split s covers keys [s*chunk, min(seq, (s+1)*chunk)), chunk =
+// ceil(seq / ATTN_SPLITS).  Per tile of AT_T keys: lane l scores key l%32
+// over dims [(l/32)*64, +64) (halves joined by one shuffle), an online
+// softmax update, then lane l accumulates P.V for dims 2l, 2l+1.  The next
+// tile's loads are in flight while the current one is computed.
+template <typename KVT>
 __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+  using G = KvTile<KVT>;
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = kvh * (NH / NKV) + wave;
@@ -456,49 +487,56 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   const int chunk = (seq + ATTN_SPLITS - 1) / ATTN_SPLITS;
   const int p0 = split * chunk, p1 = min(seq, p0 + chunk);
   __shared__ __attribute__((aligned(16))) float qs[4][HD];
-  __shared__ float ps[4][64];
+  __shared__ __attribute__((aligned(16))) KVT ks[AT_T * G::LDW];
+  __shared__ __attribute__((aligned(16))) KVT vs[AT_T * G::LDW];
+  __shared__ float ps[4][AT_T];
   const float scale = 1.0f / sqrtf((float)HD);
-  const uint16_t *Kb = a.kc + (size_t)kvh * a.max_seq * HD;
-  const uint16_t *Vb = a.vc + (size_t)kvh * a.max_seq * HD;
+  const KVT *Kb = (const KVT *)a.kc + (size_t)kvh * a.max_seq * HD;
+  const KVT *Vb = (const KVT *)a.vc + (size_t)kvh * a.max_seq * HD;
 
+  u32x4 kr[G::CPT], vr[G::CPT];
+  if (p0 < p1) attn_load_tile<KVT>(Kb, Vb, p0, min(AT_T, p1 - p0), tid, kr, vr);
   qs[wave][lane * 2] = a.q[h * HD + lane * 2];
   qs[wave][lane * 2 + 1] = a.q[h * HD + lane * 2 + 1];
-  __syncthreads();
 
+  const int key = lane & (AT_T - 1), half = lane >> 5;
   float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int pb = p0; pb < p1; pb += 64) {
-    const int n = min(64, p1 - pb);
-    const int p = pb + min(lane, n - 1);  // lanes past n re-read a valid row
-    u32x4 kr[HD / 8];
-    const u32x4 *kp = (const u32x4 *)(Kb + (size_t)p * HD);
+  for (int pb = p0; pb < p1; pb += AT_T) {
+    const int n = min(AT_T, p1 - pb);
+    __syncthreads();  // the previous tile's LDS reads are done
 #pragma unroll
-    for (int c = 0; c < HD / 8; c++) kr[c] = kp[c];
-    uint32_t vv[64];
-    const uint16_t *vp = Vb + (size_t)pb * HD + lane * 2;
-#pragma unroll
-    for (int j = 0; j < 64; j++) vv[j] = *(const uint32_t *)(vp + (size_t)min(j, n - 1) * HD);
+    for (int i = 0; i < G::CPT; i++) {
+      const int id = tid + 256 * i, row = id / G::CPR, col = id % G::CPR;
+      *(u32x4 *)(ks + row * G::LDW + col * G::EPC) = kr[i];
+      *(u32x4 *)(vs + row * G::LDW + col * G::EPC) = vr[i];
+    }
+    if (pb + AT_T < p1) attn_load_tile<KVT>(Kb, Vb, pb + AT_T, min(AT_T, p1 - pb - AT_T), tid, kr, vr);
+    __syncthreads();
+
     float dot = 0.f;
+    const KVT *kp = ks + key * G::LDW + half * (HD / 2);
+    const float *qp = &qs[wave][half * (HD / 2)];
 #pragma unroll
-    for (int c = 0; c < HD / 8; c++)
-      dot = dot8(kr[c], *(const f32x4 *)&qs[wave][c * 8], *(const f32x4 *)&qs[wave][c * 8 + 4], dot);
-    const float s = lane < n ? dot * scale : -INFINITY;
+    for (int c = 0; c < HD / 2; c += G::EPC) dot = kdot(kp + c, qp + c, dot);
+    dot += __shfl_xor(dot, 32, 64);
+    const bool valid = key < n;
+    const float s = valid ? dot * scale : -INFINITY;
     const float mnew = fmaxf(m, wave_max(s));
-    const float e = lane < n ? expf(s - mnew) : 0.f;
+    const float e = valid ? expf(s - mnew) : 0.f;
     const float corr = expf(m - mnew);
-    l = l * corr + wave_sum(e);
+    l = l * corr + wave_sum(half ? 0.f : e);
     o0 *= corr;
     o1 *= corr;
-    ps[wave][lane] = e;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 64; j++) {
-      const h2 v = __builtin_bit_cast(h2, vv[j]);
-      const float ej = ps[wave][j];  // 0 for j >= n
-      o0 = fmaf(ej, (float)v.x, o0);
-      o1 = fmaf(ej, (float)v.y, o1);
-    }
-    __syncthreads();
     m = mnew;
+    if (!half) ps[wave][key] = e;
+    __syncthreads();
+#pragma unroll 8
+    for (int j = 0; j < AT_T; j++) {
+      const float ej = ps[wave][j];  // 0 for j >= n
+      const float2 v = vpair(vs + j * G::LDW + lane * 2);
+      o0 = fmaf(ej, v.x, o0);
+      o1 = fmaf(ej, v.y, o1);
+    }
   }
   float *pp = a.part + ((size_t)h * ATTN_SPLITS + split) * (HD + 2);
   pp[lane * 2] = o0;
@@ -634,15 +672,25 @@ __global__ void gen_f16_kernel(uint16_t *out, size_t n, uint64_t seed, uint64_t 
 }
 
 // KV rows for positions [0, npos): element (pos, c) of the reference layout
-// [pos][1024] -> head-major cache [c/128][pos][c%128].
-__global__ void gen_kv_kernel(uint16_t *cache, int max_seq, int npos, uint64_t seed,
-                              uint64_t stream) {
+// [pos][1024] -> head-major cache [c/128][pos][c%128].  Values are the f16
+// generator output (N(0,1) rounded to f16), held exactly in either cache type.
+__device__ __forceinline__ float h2f_exact(uint16_t h) {  // subnormals kept
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3ffu;
+  if (e == 0) return __builtin_bit_cast(float, sign) + (sign ? -1.f : 1.f) * (float)m * 0x1p-24f;
+  if (e == 31) return __builtin_bit_cast(float, sign | 0x7f800000u | (m << 13));
+  return __builtin_bit_cast(float, sign | ((e + 112u) << 23) | (m << 13));
+}
+__device__ __forceinline__ void kv_put(float *p, uint16_t h) { *p = h2f_exact(h); }
+__device__ __forceinline__ void kv_put(uint16_t *p, uint16_t h) { *p = h; }
+template <typename KVT>
+__global__ void gen_kv_kernel(KVT *cache, int max_seq, int npos, uint64_t seed, uint64_t stream) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   size_t n = (size_t)npos * KVD;
   size_t stride = (size_t)gridDim.x * blockDim.x;
   for (; i < n; i += stride) {
     int p = (int)(i / KVD), c = (int)(i % KVD);
-    cache[((size_t)(c >> 7) * max_seq + p) * HD + (c & 127)] = f2h_exact(normal_variate(seed, stream, i));
+    kv_put(cache + ((size_t)(c >> 7) * max_seq + p) * HD + (c & 127),
+           f2h_exact(normal_variate(seed, stream, i)));
   }
 }
 

@@ -41,6 +41,7 @@ class Config(ctypes.Structure):
         ("nfe", ctypes.c_int32), ("cfg_alpha", ctypes.c_float),
         ("n_acoustic_out", ctypes.c_int32), ("semantic_vocab", ctypes.c_int32),
         ("acoustic_levels", ctypes.c_int32), ("audio_vocab", ctypes.c_int32),
+        ("kv_f16", ctypes.c_int32),  # KV cache element type: 0 f32 (reference), 1 f16
     ]
 
 
@@ -218,16 +219,16 @@ class VoxtralEngine:
     def position(self, p):
         self._check(self._lib.vx_set_position(self._h, int(p)))
 
-    def write_kv(self, layer, which, pos0, f16_bits):
-        a = np.ascontiguousarray(f16_bits)
-        a = a.view(np.uint16) if a.dtype == np.float16 else a
+    def write_kv(self, layer, which, pos0, rows):
+        """rows: [npos, n_kv_heads*head_dim] values (f32; an f16 cache rounds)."""
+        a = np.ascontiguousarray(rows, np.float32)
         kvd = self.config.n_kv_heads * self.config.head_dim
         npos = a.size // kvd
         self._check(self._lib.vx_write_kv(self._h, layer, which, pos0, npos, a.ctypes.data))
 
     def read_kv(self, layer, which, pos0, npos):
         kvd = self.config.n_kv_heads * self.config.head_dim
-        out = np.empty((npos, kvd), np.uint16)
+        out = np.empty((npos, kvd), np.float32)
         self._check(self._lib.vx_read_kv(self._h, layer, which, pos0, npos, out.ctypes.data))
         return out
 
