@@ -40,6 +40,21 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (counters scaled by a device copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "backbone_gemv_ctx512_pmc_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if parts[:2] == ["traffic_bytes_per_launch", kernel]:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def kv_bytes_per_key(kv_elem):
     return LAYERS * 2 * 1024 * kv_elem    # K and V rows of every layer
 
@@ -98,12 +113,26 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-frames", action="store_true")
     ap.add_argument("--no-f16-kv", action="store_true", help="skip the f16-KV-cache variant")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="also run a plain device copy of this many MB (a known-traffic "
+                         "kernel for scaling hardware byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the frame loop runs on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured path); use --gpus 1",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_probe_mb:
+        import torch
+        n = args.copy_probe_mb * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log(f"[gpu] copy probe: 3 x {args.copy_probe_mb} MB device copy")
 
     import voxtral_amd as V
     t0 = time.time()
@@ -128,8 +157,9 @@ def main():
         log(f"[gpu] kernel {name:7s} {us:8.2f} us  {b / 1e6:8.2f} MB  {kern[name]['GBps']:7.0f} GB/s")
     dom = kern["gateup"]
     roofline = {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": "gemv_kernel<gate/up + RMSNorm + SwiGLU>", "launch_bytes": dom["bytes"],
+                "unit": "GB/s", "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4),
+                "traffic": measured_traffic("gateup"),
+                "kernel": "gemv1_kernel<gate/up + RMSNorm + SwiGLU>", "launch_bytes": dom["bytes"],
                 "avg_us": round(dom["avg_us"], 3)}
 
     # ---- full frame loop (backbone + FM CFG Euler loop), 500 frames

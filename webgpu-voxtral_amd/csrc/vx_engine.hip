@@ -153,15 +153,14 @@ GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, in
 }  // namespace
 
 // Streaming GEMV launch: M units split exactly into blocks of WAVES*UPW.
-template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K>
+template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K, int D = 2>
 void launch_gemv1(hipStream_t st, const GemvArgs &a) {
   constexpr int per_block = WAVES * UPW;
-  hipLaunchKernelGGL((gemv1_kernel<WAVES, UPW, UPG, EPI, NORM, K>), dim3(a.M / per_block),
+  hipLaunchKernelGGL((gemv1_kernel<WAVES, UPW, UPG, EPI, NORM, K, D>), dim3(a.M / per_block),
                      dim3(WAVES * 64), 0, st, a);
 }
 // unit counts of the backbone GEMVs must split into whole blocks
-static_assert((QKV_ROWS / 2) % (6 * 2) == 0 && DIM % (6 * 2) == 0 && HID % (12 * 3) == 0 &&
-                  DIM % 12 == 0,
+static_assert((QKV_ROWS / 2) % 6 == 0 && DIM % 12 == 0 && HID % (12 * 3) == 0 && DIM % 6 == 0,
               "launch shapes");
 
 // One backbone layer: 6 launches (norm + QKV + rope + KV write | attention
@@ -180,7 +179,7 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
     a.kv_f32 = e->kv_f32;
     a.max_seq = e->max_seq;
     a.theta = e->cfg.rope_theta;
-    launch_gemv1<6, 2, 1, EPI_QKV_ROPE, true, DIM>(st, a);
+    launch_gemv1<6, 1, 1, EPI_QKV_ROPE, true, DIM, 1>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_ATTN) {
     AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn};
@@ -192,18 +191,18 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
     GemvArgs a = gargs(W.wo, e->attn, QD, e->x, 0, DIM);
-    launch_gemv1<6, 2, 1, EPI_RESID, false, QD>(st, a);
+    launch_gemv1<12, 1, 1, EPI_RESID, false, QD, 1>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_GATEUP) {
     GemvArgs a = gargs(W.w1, e->x, DIM, e->act, 0, HID);
     a.W2 = W.w3;
     a.norm_w = W.ffn_norm;
     a.eps = e->cfg.norm_eps;
-    launch_gemv1<12, 3, 1, EPI_SWIGLU, true, DIM>(st, a);
+    launch_gemv1<12, 3, 1, EPI_SWIGLU, true, DIM, 2>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_DOWN) {
     GemvArgs a = gargs(W.w2, e->act, HID, e->x, 0, DIM);
-    launch_gemv1<12, 1, 1, EPI_RESID, false, HID>(st, a);
+    launch_gemv1<6, 1, 1, EPI_RESID, false, HID, 1>(st, a);
   }
 }
 
@@ -1069,6 +1068,7 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
     stats->total_ms = ms(t0, t2);
     stats->frames_generated = frames;
   }
+  HIPCHK(e, hipStreamSynchronize(e->st));
   return VX_OK;
 }
 

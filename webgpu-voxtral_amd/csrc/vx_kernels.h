@@ -282,13 +282,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 }
 
 // ------------------------------------------------- streaming GEMV (batch 1)
-// The backbone GEMVs.  One block per CU (grid = number of CUs); block b owns
-// units [b*WAVES*UPW, (b+1)*WAVES*UPW) and wave w a contiguous run of UPW
-// units, processed in groups of UPG units.  A unit is one output row, or a
-// row pair for EPI_SWIGLU (gate row i, up row i) and EPI_QKV_ROPE (rows 2i,
-// 2i+1).  Weights do not depend on the activations, so every wave issues
-// its first group's 16-byte loads before the block stages the (normalised)
-// input vector into LDS, and loads group g+1 while it computes group g.
+// The backbone GEMVs.  Block b owns units [b*WAVES*UPW, (b+1)*WAVES*UPW) and
+// wave w a contiguous run of UPW units, processed in groups of UPG units.  A
+// unit is one output row, or a row pair for EPI_SWIGLU (gate row i, up row
+// i) and EPI_QKV_ROPE (rows 2i, 2i+1).  Per-wave loads return in issue
+// order, so the block first issues its share of the input vector (and the
+// RMSNorm gains), then the weight loads of the first D groups; the
+// normalised vector is staged into LDS while the weights are in flight, and
+// group g+D is issued as soon as group g has been consumed.
 template <int EPI>
 constexpr int rows_per_unit() {
   return (EPI == EPI_SWIGLU || EPI == EPI_QKV_ROPE) ? 2 : 1;
@@ -317,7 +318,8 @@ __device__ __forceinline__ void load_group(const GemvArgs &a, int unit0, int lan
 
 // epilogue of one unit; y[r] = full dot product of the unit's row r
 template <int EPI>
-__device__ __forceinline__ void unit_epilogue(const GemvArgs &a, int unit, const float *y, int pos) {
+__device__ __forceinline__ void unit_epilogue(const GemvArgs &a, int unit, const float *y, int pos,
+                                              float resid) {
   if (EPI == EPI_SWIGLU) {
     const float g = y[0];
     a.out[unit] = (g / (1.0f + expf(-g))) * y[1];
@@ -340,36 +342,53 @@ __device__ __forceinline__ void unit_epilogue(const GemvArgs &a, int unit, const
       kv_store2(a.vc, a.kv_f32, a.max_seq, row - QD - KVD, pos, y0, y1);
     }
   } else if (EPI == EPI_RESID) {
-    a.out[unit] = y[0] + a.out[unit];
+    a.out[unit] = y[0] + resid;
   } else {
     a.out[unit] = y[0];
   }
 }
 
-template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K>
+template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K, int D>
 __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(GemvArgs a) {
-  static_assert(K % 512 == 0 && UPW % UPG == 0, "shape");
   constexpr int RU = rows_per_unit<EPI>();
   constexpr int RG = UPG * RU;  // rows per group
   constexpr int NCH = K / 512;
   constexpr int G = UPW / UPG;
   constexpr int NT = WAVES * 64;
+  constexpr int XPT = (K + NT * 4 - 1) / (NT * 4);  // input float4s per thread
+  constexpr int DD = D < G ? D : G;                  // groups in flight
+  static_assert(K % 512 == 0 && UPW % UPG == 0 && D >= 1, "shape");
   __shared__ __attribute__((aligned(16))) float xl[K];
   __shared__ float red[WAVES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int u0 = (blockIdx.x * WAVES + wave) * UPW;
 
-  u32x4 wbuf[2][RG][NCH];
-  load_group<EPI, K, UPG>(a, u0, lane, wbuf[0]);
+  // the residual values are read first of all, so the epilogue waits on none
+  float resid[UPW];
+#pragma unroll
+  for (int u = 0; u < UPW; u++) resid[u] = EPI == EPI_RESID ? a.out[u0 + u] : 0.f;
+  f32x4 xv[XPT];
+  uint2 gv[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; i++) {
+    const int k = (tid + i * NT) * 4;
+    if (k < K) {
+      xv[i] = *(const f32x4 *)(a.x + k);
+      if (NORM) gv[i] = *(const uint2 *)(a.norm_w + k);
+    }
+  }
+  u32x4 wbuf[DD][RG][NCH];
+#pragma unroll
+  for (int g = 0; g < DD; g++) load_group<EPI, K, UPG>(a, u0 + g * UPG, lane, wbuf[g]);
 
-  // stage the input vector (RMSNorm'd: x * rms * w) while the loads fly
+  // stage the input vector (RMSNorm'd: x * rms * w) while the weights fly
   float scale = 1.0f;
   if (NORM) {
     float s = 0.f;
-    for (int i = tid * 4; i < K; i += NT * 4) {
-      f32x4 v = *(const f32x4 *)(a.x + i);
-      s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
+#pragma unroll
+    for (int i = 0; i < XPT; i++)
+      if ((tid + i * NT) * 4 < K)
+        s += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
     s = wave_sum(s);
     if (lane == 0) red[wave] = s;
     __syncthreads();
@@ -378,23 +397,26 @@ __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(GemvArgs a) {
     for (int w = 0; w < WAVES; w++) tot += red[w];
     scale = 1.0f / sqrtf(tot / (float)K + a.eps);
   }
-  for (int i = tid * 4; i < K; i += NT * 4) {
-    f32x4 v = *(const f32x4 *)(a.x + i);
-    if (NORM) {
-      const uint16_t *g = a.norm_w + i;
-      v.x = v.x * scale * h2f(g[0]);
-      v.y = v.y * scale * h2f(g[1]);
-      v.z = v.z * scale * h2f(g[2]);
-      v.w = v.w * scale * h2f(g[3]);
+#pragma unroll
+  for (int i = 0; i < XPT; i++) {
+    const int k = (tid + i * NT) * 4;
+    if (k < K) {
+      f32x4 v = xv[i];
+      if (NORM) {
+        const h2 g01 = __builtin_bit_cast(h2, gv[i].x), g23 = __builtin_bit_cast(h2, gv[i].y);
+        v.x = v.x * scale * (float)g01.x;
+        v.y = v.y * scale * (float)g01.y;
+        v.z = v.z * scale * (float)g23.x;
+        v.w = v.w * scale * (float)g23.y;
+      }
+      *(f32x4 *)(xl + k) = v;
     }
-    *(f32x4 *)(xl + i) = v;
   }
   __syncthreads();
   const int pos = (EPI == EPI_QKV_ROPE) ? *a.pos : 0;
 
 #pragma unroll
   for (int g = 0; g < G; g++) {
-    if (g + 1 < G) load_group<EPI, K, UPG>(a, u0 + (g + 1) * UPG, lane, wbuf[(g + 1) & 1]);
     float acc[RG];
 #pragma unroll
     for (int r = 0; r < RG; r++) acc[r] = 0.f;
@@ -403,13 +425,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(GemvArgs a) {
       const float *xp = xl + c * 512 + lane * 8;
       const f32x4 xa = *(const f32x4 *)xp, xb = *(const f32x4 *)(xp + 4);
 #pragma unroll
-      for (int r = 0; r < RG; r++) acc[r] = dot8(wbuf[g & 1][r][c], xa, xb, acc[r]);
+      for (int r = 0; r < RG; r++) acc[r] = dot8(wbuf[g % DD][r][c], xa, xb, acc[r]);
     }
+    if (g + DD < G) load_group<EPI, K, UPG>(a, u0 + (g + DD) * UPG, lane, wbuf[g % DD]);
 #pragma unroll
     for (int r = 0; r < RG; r++) acc[r] = wave_sum(acc[r]);
     if (lane == 0) {
 #pragma unroll
-      for (int u = 0; u < UPG; u++) unit_epilogue<EPI>(a, u0 + g * UPG + u, acc + u * RU, pos);
+      for (int u = 0; u < UPG; u++)
+        unit_epilogue<EPI>(a, u0 + g * UPG + u, acc + u * RU, pos, resid[g * UPG + u]);
     }
   }
 }
