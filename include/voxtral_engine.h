@@ -94,7 +94,7 @@ int vx_init_synthetic(vx_engine *e, uint64_t seed, float std);
  * plumbing for generator and loader checks). */
 int vx_read_tensor(vx_engine *e, const char *name, uint16_t *f16, size_t numel);
 
-/* isReady getter, src/engine.ts:2047-2049.  1 when every weight is loaded. */
+/* isReady getter, src/engine.ts:2054-2056.  1 when every weight is loaded. */
 int vx_is_ready(const vx_engine *e);
 
 /* reset(), src/engine.ts:2323-2327: position = 0 (stale KV is never read). */

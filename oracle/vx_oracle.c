@@ -24,7 +24,8 @@
  *   cfg / euler           closed forms; v_c == v_u gives v; v = 0 is a no-op
  *   fsq                   known answers -1 -> 2, 0 -> 12, +1 -> 22, ties to
  *                         even, clamping
- *   argmax                numpy argmax (first max) on tie-free and tied data
+ *   argmax                numpy argmax on tie-free data; exact ties against
+ *                         a hand trace of the 256-lane tree rule
  *   multi-codebook embed  row formula 8194 + k*23 + code, f64 sum
  *   bi-attention          torch SDPA over 3 tokens (f64)
  *   backbone step         a float64 numpy transformer layer written from the

@@ -1,0 +1,90 @@
+"""The Node-API binding (webgpu-voxtral_amd/napi): the reference's
+VoxtralEngine surface in Node over the C ABI.  CPU: the addon loads and
+exports the API, and library errors arrive as JS Errors.  GPU: generate()
+through Node equals generate() through the Python binding, with every
+onFrame call delivered before the promise settles (src/engine.ts:2584)."""
+import json
+import os
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+JS = os.path.join(ROOT, "webgpu-voxtral_amd", "napi", "voxtral_engine.js")
+ADDON = os.path.join(ROOT, "webgpu-voxtral_amd", "lib", "voxtral_napi.node")
+
+pytestmark = pytest.mark.skipif(shutil.which("node") is None or not os.path.exists(ADDON),
+                                reason="node or the built addon is not available")
+
+
+def run_node(script, timeout=120):
+    p = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=timeout,
+                       cwd=ROOT)
+    assert p.returncode == 0, p.stderr
+    return p.stdout
+
+
+def test_addon_exports_and_errors():
+    out = run_node(f"""
+const m = require({json.dumps(JS)});
+const names = Object.keys(m.native).sort();
+const e = new m.VoxtralEngine({{config: {{backbone: {{n_layers: 1}}}}, maxSeqLen: 64}});
+let ready = e.isReady;
+let msg = '';
+try {{ e.reset(); }} catch (err) {{ msg = err.message; }}
+e.init().then(() => console.log(JSON.stringify({{names, ready, msg, init: 'ok'}})),
+              (err) => console.log(JSON.stringify({{names, ready, msg, init: err.message}})));
+""")
+    r = json.loads(out.strip().splitlines()[-1])
+    assert r["names"] == sorted(["create", "destroy", "loadTensor", "initSynthetic", "isReady",
+                                 "reset", "position", "backboneStep", "fmForward",
+                                 "setSemanticCode", "read", "generate"])
+    assert r["ready"] is False
+    assert r["msg"].startswith("Engine not initialized")
+    # without a GPU the library's own error; with one, init succeeds
+    assert r["init"] in ("ok", "No HIP device")
+
+
+@pytest.mark.gpu
+def test_generate_through_node_matches_python():
+    tokens = [1, 25, 24, 24, 35, 500, 24]
+    voice = 7
+    script = f"""
+const m = require({json.dumps(JS)});
+(async () => {{
+  const e = new m.VoxtralEngine({{config: {{backbone: {{n_layers: 2}}}}, maxSeqLen: 64}});
+  await e.init();
+  e.initSynthetic(0, 0.02);
+  const voice = new Float32Array(2 * 3072);
+  for (let i = 0; i < voice.length; i++) voice[i] = ((i * {voice}) % 13 - 6) * 0.0625;
+  const frames = [];
+  const stages = [];
+  let settled = false, late = 0;
+  const r = await e.generate({json.dumps(tokens)}, 2, 2, voice, 5,
+    (f, s, codes) => {{ if (settled) late++; frames.push([f, s, Array.from(codes)]); }},
+    (st, ms) => stages.push([st, ms === undefined ? null : 1]),
+    {{sampling: 'greedy', seed: 3, ignoreEos: true}});
+  settled = true;
+  const normed = await e.debugBackboneStepFull(24);
+  e.destroy();
+  console.log(JSON.stringify({{sem: r.semanticCodes, ac: r.acousticCodes, n: r.stats.framesGenerated,
+                               frames, stages, late, audio: r.audio.length, normed0: normed[0]}}));
+}})().catch((err) => {{ console.error(err); process.exit(3); }});
+"""
+    print("[napi] node generate, 2 layers, 5 frames", flush=True)
+    r = json.loads(run_node(script, timeout=300).strip().splitlines()[-1])
+
+    import numpy as np
+    import voxtral_amd as V
+    g = V.VoxtralEngine(V.default_config(n_layers=2), max_seq_len=64).init()
+    try:
+        g.init_synthetic(0, 0.02)
+        vo = (((np.arange(2 * 3072) * voice) % 13 - 6) * 0.0625).astype(np.float32)  # exact in both
+        py = g.generate(tokens, 2, 2, vo, 5, sampling="greedy", seed=3, ignore_eos=True)
+    finally:
+        g.destroy()
+    assert r["n"] == 5 and r["sem"] == py["semanticCodes"] and r["ac"] == py["acousticCodes"]
+    assert [f[0] for f in r["frames"]] == list(range(5)) and r["late"] == 0
+    assert [f[1] for f in r["frames"]] == r["sem"] and [f[2] for f in r["frames"]] == r["ac"]
+    assert r["stages"][0] == ["backbone", None] and r["audio"] == 0

@@ -1,0 +1,73 @@
+// Types of voxtral_engine.js: the reference's VoxtralEngine surface
+// (src/engine.ts:213-237, 291-2632) for the per-frame token loop.
+
+export interface VoxtralConfig {
+  backbone?: {
+    dim?: number; n_layers?: number; head_dim?: number; hidden_dim?: number;
+    n_heads?: number; n_kv_heads?: number; vocab_size?: number;
+    rope_theta?: number; norm_eps?: number;
+  };
+  fm?: { n_layers?: number; nfe?: number; cfg_alpha?: number };
+  /** KV cache element type: false f32 (the reference's), true f16 */
+  kvF16?: boolean;
+}
+
+export interface EngineOptions {
+  config?: VoxtralConfig;
+  maxSeqLen?: number;
+}
+
+export interface TTSResult {
+  semanticCodes: number[];
+  acousticCodes: number[][];
+  /** empty: the codec decoder is outside this library */
+  audio: Float32Array;
+  stats: {
+    backboneMs: number;
+    fmMs: number;
+    codecMs: number;
+    totalMs: number;
+    framesGenerated: number;
+  };
+}
+
+export interface GenerateOptions {
+  sampling?: 'top_p' | 'greedy';
+  topP?: number;
+  temperature?: number;
+  seed?: number;
+  ignoreEos?: boolean;
+}
+
+export declare class VoxtralEngine {
+  constructor(options?: EngineOptions);
+  init(): Promise<void>;
+  loadWeights(baseUrl?: string): Promise<void>;
+  loadWeightsFromHF(url?: string): Promise<void>;
+  loadTensor(name: string, f16: Uint16Array, shape: number[]): void;
+  initSynthetic(seed?: number, std?: number): void;
+  readonly isReady: boolean;
+  position: number;
+  reset(): void;
+  debugRead(bufferName: string, count?: number): Promise<Float32Array>;
+  backboneStepAndRead(tokenId: number, useAudioEmbedding?: boolean): Promise<number>;
+  debugBackboneStepFull(tokenId: number, useAudioEmbedding?: boolean): Promise<Float32Array>;
+  backboneStepEmbedding(embedding: Float32Array): Promise<Float32Array>;
+  debugFMStep(debugNoise?: Float32Array): Promise<{
+    semantic_logits: Float32Array;
+    acoustic_codes: Uint32Array;
+    x_final: Float32Array;
+  }>;
+  fmStepAndRead(): Promise<Uint32Array>;
+  generate(
+    tokens: number[],
+    audioTokenStart: number,
+    audioTokenCount: number,
+    voiceEmbeddings: Float32Array | null,
+    maxFrames?: number,
+    onFrame?: (frame: number, semanticCode: number, acousticCodes: Uint32Array) => void,
+    onStage?: (stage: 'backbone' | 'fm' | 'codec', doneMs?: number) => void,
+    options?: GenerateOptions,
+  ): Promise<TTSResult>;
+  destroy(): void;
+}

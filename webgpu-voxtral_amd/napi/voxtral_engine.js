@@ -1,0 +1,153 @@
+'use strict';
+// VoxtralEngine over the MI355X HIP engine: the public surface of the
+// reference's class (src/engine.ts:291-2632, types src/engine.ts:213-237)
+// implemented on the Node-API addon voxtral_napi.node, which calls the C ABI
+// of libvoxtral_amd.so (include/voxtral_engine.h).  Plain ES2019 so that it
+// runs on the Node 12 of this image; voxtral_engine.d.ts carries the types.
+const path = require('path');
+
+const ADDON = process.env.VOXTRAL_NAPI || path.join(__dirname, '..', 'lib', 'voxtral_napi.node');
+const native = require(ADDON);
+
+const EMBED_TOKEN = 0;
+const EMBED_AUDIO = 1;
+const EMBED_PRECOMPUTED = 2;
+
+// reference defaultConfig (src/types.ts:70-122), the fields the engine reads
+function flattenConfig(config) {
+  if (!config) return null;
+  const b = config.backbone || {};
+  const fm = config.fm || {};
+  const out = {};
+  const put = (k, v) => { if (v !== undefined) out[k] = v; };
+  put('dim', b.dim);
+  put('nLayers', b.n_layers);
+  put('headDim', b.head_dim);
+  put('hiddenDim', b.hidden_dim);
+  put('nHeads', b.n_heads);
+  put('nKvHeads', b.n_kv_heads);
+  put('vocabSize', b.vocab_size);
+  put('ropeTheta', b.rope_theta);
+  put('normEps', b.norm_eps);
+  put('fmLayers', fm.n_layers);
+  put('nfe', fm.nfe);
+  put('cfgAlpha', fm.cfg_alpha);
+  put('kvF16', config.kvF16 ? 1 : undefined);
+  return out;
+}
+
+class VoxtralEngine {
+  /** new VoxtralEngine({config?, maxSeqLen? = 4096}), src/engine.ts:301-304 */
+  constructor(options) {
+    options = options || {};
+    this.config = options.config || null;
+    this.maxSeqLen = options.maxSeqLen || 4096;
+    this._h = null;
+  }
+
+  /** init(), src/engine.ts:313: device + buffers (weights arrive next) */
+  async init() {
+    if (this._h) return;
+    this._h = native.create(flattenConfig(this.config), this.maxSeqLen);
+  }
+
+  _handle() {
+    if (!this._h) throw new Error('Engine not initialized. Call init() and loadWeights() first.');
+    return this._h;
+  }
+
+  /** loadWeights(baseUrl) fetches over HTTP (src/engine.ts:539-566); this
+   *  build has no network path: pass tensors with loadTensor(). */
+  async loadWeights() {
+    throw new Error('loadWeights: no network loader in this build; use loadTensor(name, f16, shape)');
+  }
+
+  async loadWeightsFromHF() {
+    return this.loadWeights();
+  }
+
+  /** one tensor of organizeWeights (src/engine.ts:659-743): f16 bits */
+  loadTensor(name, f16, shape) {
+    native.loadTensor(this._handle(), name, f16, shape);
+  }
+
+  /** every weight from the portable seeded generator (tests, benchmarks) */
+  initSynthetic(seed, std) {
+    native.initSynthetic(this._handle(), seed || 0, std === undefined ? 0.02 : std);
+  }
+
+  /** isReady, src/engine.ts:2054-2056 */
+  get isReady() {
+    return this._h !== null && native.isReady(this._h);
+  }
+
+  get position() {
+    return native.position(this._handle());
+  }
+
+  set position(p) {
+    native.position(this._handle(), p);
+  }
+
+  /** reset(), src/engine.ts:2323-2327 */
+  reset() {
+    native.reset(this._handle());
+  }
+
+  /** debugRead(name, count), src/engine.ts:2062-2067 */
+  async debugRead(bufferName, count) {
+    return native.read(this._handle(), bufferName, count === undefined ? 16 : count);
+  }
+
+  /** backboneStepAndRead, src/engine.ts:2333-2342: LM-head argmax */
+  async backboneStepAndRead(tokenId, useAudioEmbedding) {
+    const mode = useAudioEmbedding ? EMBED_AUDIO : EMBED_TOKEN;
+    return native.backboneStep(this._handle(), tokenId, mode, null, true).argmax;
+  }
+
+  /** debugBackboneStepFull, src/engine.ts:2348-2357: W.normed */
+  async debugBackboneStepFull(tokenId, useAudioEmbedding) {
+    const mode = useAudioEmbedding ? EMBED_AUDIO : EMBED_TOKEN;
+    return native.backboneStep(this._handle(), tokenId, mode, null, false).normed;
+  }
+
+  /** backbone step on a precomputed embedding (src/engine.ts:847-854) */
+  async backboneStepEmbedding(embedding) {
+    return native.backboneStep(this._handle(), 0, EMBED_PRECOMPUTED, embedding, false).normed;
+  }
+
+  /** debugFMStep(debugNoise?), src/engine.ts:2363-2380 */
+  async debugFMStep(debugNoise) {
+    const r = native.fmForward(this._handle(), debugNoise || null);
+    return { semantic_logits: r.semanticLogits, acoustic_codes: r.acousticCodes, x_final: r.xFinal };
+  }
+
+  /** fmStepAndRead, src/engine.ts:2386-2396 */
+  async fmStepAndRead() {
+    return native.fmForward(this._handle(), null).acousticCodes;
+  }
+
+  /**
+   * generate(tokens, audioTokenStart, audioTokenCount, voiceEmbeddings,
+   * maxFrames = 500, onFrame?, onStage?), src/engine.ts:2416-2616.  The codec
+   * decoder is outside this library: `audio` is empty.  `options` (not in
+   * the reference) selects sampling 'top_p' (default, the reference's) or
+   * 'greedy', the seed that replaces Math.random, and ignoreEos.
+   */
+  async generate(tokens, audioTokenStart, audioTokenCount, voiceEmbeddings, maxFrames,
+    onFrame, onStage, options) {
+    const r = await native.generate(this._handle(), tokens, audioTokenStart, audioTokenCount,
+      voiceEmbeddings || null, maxFrames === undefined ? 500 : maxFrames, options || null,
+      onFrame || null, onStage || null);
+    r.audio = new Float32Array(0);
+    return r;
+  }
+
+  /** destroy(), src/engine.ts:2621-2632 */
+  destroy() {
+    if (this._h) native.destroy(this._h);
+    this._h = null;
+  }
+}
+
+module.exports = { VoxtralEngine, native, EMBED_TOKEN, EMBED_AUDIO, EMBED_PRECOMPUTED };
