@@ -75,6 +75,13 @@ struct vx_engine {
         *fm_act = nullptr, *fm_llm_out = nullptr, *sem_logits = nullptr, *tproj = nullptr,
         *xh = nullptr, *vel = nullptr, *noise = nullptr, *time_embed = nullptr;
   bool tproj_ready = false;
+  // FM layer matrices in the MFMA A-operand order (pack_mfma_a_kernel), and
+  // the packed inputs / sums of squares the FM GEMMs hand to each other
+  void *fm_parena = nullptr;
+  std::vector<LayerW> FP;
+  bool fm_packed_ready = false;
+  h8 *fm_b_attn = nullptr, *fm_b_o = nullptr, *fm_b_ffn = nullptr, *fm_b_act = nullptr;
+  float *fm_ssq_attn = nullptr, *fm_ssq_ffn = nullptr;
 
   int host_pos = 0;
   hipGraphExec_t step_exec = nullptr, hold_exec = nullptr, frame_exec = nullptr,
@@ -152,6 +159,16 @@ GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, in
 
 }  // namespace
 
+// FM GEMM launch: `rows` output rows in tiles of 16, RG tiles per block.
+template <int EPI, int K, int RG, int KS, int P>
+void launch_gemm6(hipStream_t st, const Gemm6Args &a, int rows) {
+  hipLaunchKernelGGL((gemm6_kernel<EPI, K, RG, KS, P>), dim3(rows / (16 * RG)), dim3(RG * KS * 64),
+                     0, st, a);
+}
+static_assert(QKV_ROWS % 16 == 0 && DIM % 16 == 0 && HID % 16 == 0 && DIM / 16 <= SSQ_MAX &&
+                  DIM % 256 == 0,
+              "FM GEMM tiles");
+
 // Streaming GEMV launch: M units split exactly into blocks of WAVES*UPW.
 template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K, int D = 2>
 void launch_gemv1(hipStream_t st, const GemvArgs &a) {
@@ -221,7 +238,24 @@ static void enqueue_lm_head(vx_engine *e) {
                      e->argmax_res);
 }
 
+// Before an FM pass: the time-projection table of the nfe-1 timesteps and
+// the MFMA-order copies of the FM layer matrices (redone after any load).
 static int ensure_tproj(vx_engine *e) {
+  if (!e->fm_packed_ready) {
+    auto pack = [&](const uint16_t *src, uint16_t *dst, int M, int K) {
+      hipLaunchKernelGGL(pack_mfma_a_kernel, dim3(2048), dim3(256), 0, e->st, src, dst, M, K);
+    };
+    for (size_t l = 0; l < e->FL.size(); l++) {
+      const LayerW &W = e->FL[l], &P = e->FP[l];
+      pack(W.wqkv, P.wqkv, QKV_ROWS, DIM);
+      pack(W.wo, P.wo, DIM, QD);
+      pack(W.w1, P.w1, HID, DIM);
+      pack(W.w3, P.w3, HID, DIM);
+      pack(W.w2, P.w2, DIM, HID);
+    }
+    LAUNCHCHK(e);
+    e->fm_packed_ready = true;
+  }
   if (e->tproj_ready) return VX_OK;
   for (int s = 0; s < e->nsteps(); s++) {
     float t = (float)((double)s / (double)(e->cfg.nfe - 1));
@@ -252,35 +286,65 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
                        greedy_code ? 8194 : 0, e->sem_code);
   }
   for (int s = 0; s < e->nsteps(); s++) {
-    FmStepArgs fa{e->xh, e->vel, e->fm_in, e->tproj + (size_t)s * DIM, e->fm_llm_out, e->fm_seq,
-                  s, alpha, dt, noise_src};
+    FmStepArgs fa{e->xh,      e->vel, e->fm_in,        e->tproj + (size_t)s * DIM,
+                  e->fm_llm_out, e->fm_seq, s, alpha, dt, noise_src, e->fm_b_attn,
+                  e->FL[0].attn_norm, e->fm_ssq_attn};
     hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256), dim3(256), 0, st, fa);
+    int nssq_attn = DIM / 256;  // partial sums written by the kernel above
     for (int l = 0; l < e->cfg.fm_layers; l++) {
-      const LayerW &W = e->FL[l];
-      {
-        GemvArgs a = gargs(W.wqkv, e->fm_seq, DIM, e->fm_q, 0, QKV_ROWS);
+      const LayerW &W = e->FL[l], &P = e->FP[l];
+      const bool last = l + 1 == e->cfg.fm_layers;
+      {  // RMSNorm + QKV (no rope: src/engine.ts:1108)
+        Gemm6Args a{};
+        a.W = P.wqkv;
+        a.B = e->fm_b_attn;
+        a.ssq = e->fm_ssq_attn;
+        a.nssq = nssq_attn;
+        a.eps = 1e-5f;
+        a.out = e->fm_q;
         a.out_k = e->fm_k;
         a.out_v = e->fm_v;
-        a.norm_w = W.attn_norm;
-        a.eps = 1e-5f;
-        launch_gemv<6, W4, 2, EPI_QKV, true, DIM, 1536>(st, a);
+        launch_gemm6<EPI_QKV, DIM, 1, 2, 12>(st, a, QKV_ROWS);
       }
       hipLaunchKernelGGL(fm_attn_kernel, dim3(NH, 2), dim3(64), 0, st, e->fm_q, e->fm_k, e->fm_v,
-                         e->fm_attn);
-      {
-        GemvArgs a = gargs(W.wo, e->fm_attn, QD, e->fm_seq, DIM, DIM);
-        launch_gemv<6, W4, 1, EPI_RESID, false, QD, 1024>(st, a);
+                         e->fm_attn, e->fm_b_o);
+      {  // O + residual; hands norm(x) * ffn gains to gate/up
+        Gemm6Args a{};
+        a.W = P.wo;
+        a.B = e->fm_b_o;
+        a.out = e->fm_seq;
+        a.os = DIM;
+        a.Bn = e->fm_b_ffn;
+        a.gn = W.ffn_norm;
+        a.ssq_out = e->fm_ssq_ffn;
+        launch_gemm6<EPI_RESID, QD, 1, 4, 16>(st, a, DIM);
       }
-      {
-        GemvArgs a = gargs(W.w1, e->fm_seq, DIM, e->fm_act, HID, HID);
-        a.W2 = W.w3;
-        a.norm_w = W.ffn_norm;
+      {  // RMSNorm + gate/up + SwiGLU; hands the activation to down
+        Gemm6Args a{};
+        a.W = P.w1;
+        a.W2 = P.w3;
+        a.B = e->fm_b_ffn;
+        a.ssq = e->fm_ssq_ffn;
+        a.nssq = DIM / 16;
         a.eps = 1e-5f;
-        launch_gemv<6, W4, 2, EPI_SWIGLU, true, DIM, 1536>(st, a);
+        a.out = e->fm_act;
+        a.os = HID;
+        a.Bn = e->fm_b_act;
+        launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 16>(st, a, HID);
       }
-      {
-        GemvArgs a = gargs(W.w2, e->fm_act, HID, e->fm_seq, DIM, DIM);
-        launch_gemv<6, W4, 1, EPI_RESID, false, HID, 1536>(st, a);
+      {  // down + residual; hands norm(x) * next attention gains to the next layer
+        Gemm6Args a{};
+        a.W = P.w2;
+        a.B = e->fm_b_act;
+        a.out = e->fm_seq;
+        a.os = DIM;
+        if (!last) {
+          a.Bn = e->fm_b_attn;
+          a.gn = e->FL[l + 1].attn_norm;
+          a.ssq_out = e->fm_ssq_attn;
+        }
+        launch_gemm6<EPI_RESID, HID, 1, 4, 24>(st, a, DIM);
+        nssq_attn = DIM / 16;
       }
     }
     {  // final norm of position 0 of each branch -> acoustic_out -> vel[s]
@@ -536,6 +600,29 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   add_slot(e, "acoustic_transformer.semantic_codebook_output.weight", e->fm_sem, {SEMV, DIM}, false);
   add_slot(e, "acoustic_transformer.acoustic_codebook_output.weight", e->fm_ac, {NAC, DIM}, false);
 
+  // ---- FM layer matrices in MFMA operand order
+  {
+    const size_t per = align256((size_t)QKV_ROWS * DIM * 2) + align256((size_t)DIM * QD * 2) +
+                       2 * align256((size_t)HID * DIM * 2) + align256((size_t)DIM * HID * 2);
+    if (hipMalloc(&e->fm_parena, per * fl) != hipSuccess) {
+      vx_destroy(e);
+      return fail(nullptr, VX_E_NOMEM, "hipMalloc of %zu packed FM weight bytes failed", per * fl);
+    }
+    e->FP.resize(fl);
+    char *p = (char *)e->fm_parena;
+    auto take = [&](uint16_t **dst, size_t elems) {
+      *dst = (uint16_t *)p;
+      p += align256(elems * 2);
+    };
+    for (auto &P : e->FP) {
+      take(&P.wqkv, (size_t)QKV_ROWS * DIM);
+      take(&P.wo, (size_t)DIM * QD);
+      take(&P.w1, (size_t)HID * DIM);
+      take(&P.w3, (size_t)HID * DIM);
+      take(&P.w2, (size_t)DIM * HID);
+    }
+  }
+
   // ---- KV cache
   size_t kvbytes = (size_t)nl * 2 * NKV * max_seq * HD * e->kv_elem;
   if (hipMalloc(&e->kv, kvbytes) != hipSuccess) {
@@ -580,6 +667,12 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   aplace((void **)&e->vel, (size_t)ns * 2 * NAC * 4);
   aplace((void **)&e->noise, NAC * 4);
   aplace((void **)&e->time_embed, DIM * 4);
+  aplace((void **)&e->fm_b_attn, (size_t)DIM / 8 * BCOL * 16);
+  aplace((void **)&e->fm_b_o, (size_t)QD / 8 * BCOL * 16);
+  aplace((void **)&e->fm_b_ffn, (size_t)DIM / 8 * BCOL * 16);
+  aplace((void **)&e->fm_b_act, (size_t)HID / 8 * BCOL * 16);
+  aplace((void **)&e->fm_ssq_attn, (size_t)SSQ_MAX * FMV * 4);
+  aplace((void **)&e->fm_ssq_ffn, (size_t)SSQ_MAX * FMV * 4);
   if (hipMalloc(&e->aarena, abytes) != hipSuccess) {
     vx_destroy(e);
     return fail(nullptr, VX_E_NOMEM, "hipMalloc of activations failed");
@@ -605,6 +698,7 @@ void vx_destroy(vx_engine *e) {
   if (e->frame_exec) (void)hipGraphExecDestroy(e->frame_exec);
   if (e->warena) (void)hipFree(e->warena);
   if (e->kv) (void)hipFree(e->kv);
+  if (e->fm_parena) (void)hipFree(e->fm_parena);
   if (e->aarena) (void)hipFree(e->aarena);
   if (e->ev0) (void)hipEventDestroy(e->ev0);
   if (e->ev1) (void)hipEventDestroy(e->ev1);
@@ -629,6 +723,7 @@ int vx_load_tensor(vx_engine *e, const char *name, const uint16_t *f16, size_t n
   HIPCHK(e, hipStreamSynchronize(e->st));
   s.loaded = true;
   if (s.ptr == e->fm_time) e->tproj_ready = false;
+  e->fm_packed_ready = false;
   return VX_OK;
 }
 
@@ -644,6 +739,7 @@ int vx_init_synthetic(vx_engine *e, uint64_t seed, float std) {
   LAUNCHCHK(e);
   HIPCHK(e, hipStreamSynchronize(e->st));
   e->tproj_ready = false;
+  e->fm_packed_ready = false;
   return VX_OK;
 }
 

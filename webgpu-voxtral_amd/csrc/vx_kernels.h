@@ -718,6 +718,192 @@ __global__ void gen_kv_kernel(KVT *cache, int max_seq, int npos, uint64_t seed, 
   }
 }
 
+// --------------------------------------------- batched GEMM on MFMA (FM)
+// The flow-matching transformer applies every weight to FMV = 6 vectors (3
+// sequence positions x conditional/unconditional), so its GEMVs are thin
+// GEMMs, out[v][row] = sum_k W[row][k] * y[v][k], run on
+// v_mfma_f32_16x16x32_f16:
+//  - A operand: the weights, pre-arranged once as [row tile][k chunk][lane][8]
+//    (rows t*16 + lane%16, k = chunk*32 + (lane/16)*8 + e), so one chunk's
+//    operand is a contiguous 1 KB read;
+//  - B operand: the packed input [k/8][BCOL] of 8-half groups, column v the
+//    hi part f16(y_v) and column FMV+v the lo part f16(y_v - hi): W is exactly
+//    f16, so D[.][v] + D[.][FMV+v] is the f32 dot product up to rounding of
+//    order 2^-22 (f16 subnormals are kept by the conversion).  Columns 12-15
+//    of D are never read.
+// The kernel that produces a GEMM's input writes this packed form in its
+// epilogue, with the next RMSNorm's gains already applied; the RMS scale
+// itself multiplies the GEMM result (W.(x*g*r) = r * W.(x*g)), from
+// per-tile sums of squares the producer also writes.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+constexpr int FMV = 6;
+constexpr int BCOL = 2 * FMV;
+constexpr int SSQ_MAX = 192;  // partial sums of squares per vector (row tiles of a DIM output)
+
+__device__ __forceinline__ void bpack_put(h8 *B, int v, int k, float y) {
+  const _Float16 hi = (_Float16)y, lo = (_Float16)(y - (float)hi);
+  _Float16 *p = (_Float16 *)(B + (k >> 3) * BCOL);
+  p[v * 8 + (k & 7)] = hi;
+  p[(FMV + v) * 8 + (k & 7)] = lo;
+}
+// four consecutive k (k % 4 == 0) of vector v
+__device__ __forceinline__ void bpack_put4(h8 *B, int v, int k, f32x4 y) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  h4 hi, lo;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    hi[j] = (_Float16)y[j];
+    lo[j] = (_Float16)(y[j] - (float)hi[j]);
+  }
+  _Float16 *p = (_Float16 *)(B + (k >> 3) * BCOL);
+  *(h4 *)(p + v * 8 + (k & 7)) = hi;
+  *(h4 *)(p + (FMV + v) * 8 + (k & 7)) = lo;
+}
+
+// W [M][K] row-major -> [M/16][K/32][64][8] (see above)
+__global__ void pack_mfma_a_kernel(const uint16_t *W, uint16_t *Wp, int M, int K) {
+  const size_t total = (size_t)M * K / 8;
+  const int nch = K / 32;
+  for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
+       q += (size_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(q & 63);
+    const size_t tc = q >> 6;
+    const int c = (int)(tc % nch);
+    const size_t tile = tc / nch;
+    const uint16_t *src = W + (tile * 16 + (lane & 15)) * K + c * 32 + (lane >> 4) * 8;
+    *(u32x4 *)(Wp + q * 8) = *(const u32x4 *)src;
+  }
+}
+
+struct Gemm6Args {
+  const uint16_t *W, *W2;  // packed A (EPI_SWIGLU: W gate, W2 up)
+  const h8 *B;             // packed input [K/8][BCOL]
+  const float *ssq;        // RMSNorm of the input: nssq partial sums of squares per
+  int nssq;                //   vector, ssq[p*FMV + v]; null: no norm
+  float eps;
+  float *out;              // outputs, vector stride os
+  int os;
+  float *out_k, *out_v;    // EPI_QKV
+  h8 *Bn;                  // optional: next GEMM's packed input from the new values
+  const uint16_t *gn;      //   times these gains (null: none)
+  float *ssq_out;          //   and their sums of squares per (row tile, vector)
+};
+
+// Block = RG row tiles x KS k-slices (one wave each); a wave streams its
+// tile's chunks (EPI_SWIGLU: the gate and up tiles), P chunks in flight, and
+// k-slices are summed through LDS.  Grid = rows / (16 RG).
+template <int EPI, int K, int RG, int KS, int P>
+__global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
+  constexpr int TL = EPI == EPI_SWIGLU ? 2 : 1;
+  constexpr int NC = K / 32, NCW = NC / KS;
+  static_assert(NC % KS == 0 && NCW % P == 0, "shape");
+  __shared__ f32x4 part[KS > 1 ? (KS - 1) * RG * TL : 1][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rg = wave / KS, kp = wave % KS;
+  const int tile = blockIdx.x * RG + rg, row0 = tile * 16, n = lane & 15;
+  const uint16_t *wp[TL];
+#pragma unroll
+  for (int t = 0; t < TL; t++) wp[t] = (t ? a.W2 : a.W) + ((size_t)tile * NC * 64 + lane) * 8;
+  // lanes of columns 12-15 read a duplicate column (their D columns are unused)
+  const h8 *bp = a.B + (lane >> 4) * BCOL + (n < BCOL ? n : n - FMV);
+  // RMS scale of each input vector from the producer's partial sums
+  // (at most SSQ_MAX per vector); loaded before the weights, whose loads
+  // return after them
+  float sv[SSQ_MAX / 64][FMV];
+  const bool norm = a.ssq != nullptr && kp == 0;
+#pragma unroll
+  for (int i = 0; i < SSQ_MAX / 64; i++)
+#pragma unroll
+    for (int v = 0; v < FMV; v++)
+      sv[i][v] = norm && lane + 64 * i < a.nssq ? a.ssq[(lane + 64 * i) * FMV + v] : 0.f;
+  u32x4 wb[P][TL];
+  h8 bb[P];
+  auto load = [&](int i, int d) {
+    const int c = kp * NCW + i;
+    bb[d] = bp[c * 4 * BCOL];
+#pragma unroll
+    for (int t = 0; t < TL; t++) wb[d][t] = *(const u32x4 *)(wp[t] + (size_t)c * 512);
+  };
+#pragma unroll
+  for (int d = 0; d < P; d++) load(d, d);
+  float rs[FMV];
+#pragma unroll
+  for (int v = 0; v < FMV; v++) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < SSQ_MAX / 64; i++) s += sv[i][v];
+    rs[v] = norm ? 1.0f / sqrtf(wave_sum(s) / (float)DIM + a.eps) : 1.0f;
+  }
+  f32x4 acc[TL];
+#pragma unroll
+  for (int t = 0; t < TL; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < NCW; c0 += P) {
+#pragma unroll
+    for (int d = 0; d < P; d++) {
+#pragma unroll
+      for (int t = 0; t < TL; t++)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, wb[d][t]), bb[d],
+                                                        acc[t], 0, 0, 0);
+      if (c0 + d + P < NCW) load(c0 + d + P, d);
+    }
+  }
+  if (KS > 1) {
+    if (kp > 0)
+#pragma unroll
+      for (int t = 0; t < TL; t++) part[((kp - 1) * RG + rg) * TL + t][lane] = acc[t];
+    __syncthreads();
+    if (kp > 0) return;
+#pragma unroll
+    for (int q = 1; q < KS; q++)
+#pragma unroll
+      for (int t = 0; t < TL; t++) acc[t] += part[((q - 1) * RG + rg) * TL + t][lane];
+  }
+  // hi + lo columns: lanes n < FMV then hold rows r..r+3 of vector v = n
+#pragma unroll
+  for (int t = 0; t < TL; t++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[t][j] += __shfl(acc[t][j], lane + FMV, 64);
+  const int v = n < FMV ? n : 0, r = row0 + 4 * (lane >> 4);
+  float rv = rs[0];
+#pragma unroll
+  for (int u = 1; u < FMV; u++) rv = v == u ? rs[u] : rv;
+  f32x4 y = acc[0] * rv;  // new values of rows r..r+3 (EPI_RESID: after the add)
+  if (n < FMV) {
+    if (EPI == EPI_SWIGLU) {
+      const f32x4 u = acc[TL - 1] * rv;
+#pragma unroll
+      for (int j = 0; j < 4; j++) y[j] = (y[j] / (1.0f + expf(-y[j]))) * u[j];
+      *(f32x4 *)(a.out + (size_t)v * a.os + r) = y;
+    } else if (EPI == EPI_RESID) {
+      f32x4 *o = (f32x4 *)(a.out + (size_t)v * a.os + r);
+      y = y + *o;
+      *o = y;
+    } else if (EPI == EPI_QKV) {
+      if (r < QD)
+        *(f32x4 *)(a.out + (size_t)v * QD + r) = y;
+      else if (r < QD + KVD)
+        *(f32x4 *)(a.out_k + (size_t)v * KVD + r - QD) = y;
+      else
+        *(f32x4 *)(a.out_v + (size_t)v * KVD + r - QD - KVD) = y;
+    } else {
+      *(f32x4 *)(a.out + (size_t)v * a.os + r) = y;
+    }
+  }
+  if (a.Bn) {  // producer side of the next GEMM
+    float s2 = n < FMV ? y[0] * y[0] + y[1] * y[1] + y[2] * y[2] + y[3] * y[3] : 0.f;
+    s2 += __shfl_xor(s2, 16, 64);
+    s2 += __shfl_xor(s2, 32, 64);
+    if (n < FMV) {
+      f32x4 z = y;
+      if (a.gn)
+#pragma unroll
+        for (int j = 0; j < 4; j++) z[j] *= h2f(a.gn[r + j]);
+      bpack_put4(a.Bn, v, r, z);
+      if (a.ssq_out && lane < 16) a.ssq_out[tile * FMV + v] = s2;
+    }
+  }
+}
+
 // ------------------------------------------------------------- FM kernels
 // timeEmbedding (src/shaders.ts:579-602) for t
 __global__ void time_embed_kernel(float *out, float t) {
@@ -747,6 +933,9 @@ struct FmStepArgs {
   int step;
   float alpha, dt;
   const float *noise;    // step 0: x_t = noise
+  h8 *Bn;                // packed input of the first layer's QKV GEMM,
+  const uint16_t *gn;    //   times its attention-norm gains,
+  float *ssq_out;        //   and sums of squares [block][FMV]
 };
 
 // Start of Euler step s: x_s (from x_{s-1} and the CFG velocity of step
@@ -767,25 +956,31 @@ __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
     if (blockIdx.x == 0) a.xh[a.step * NAC + t] = x;
   }
   __syncthreads();
-  const int row = blockIdx.x * 256 + t;
-  if (row >= DIM) return;
+  const int row = blockIdx.x * 256 + t;  // grid covers DIM exactly
   const uint16_t *w = a.w_in + (size_t)row * NAC;
   float acc = 0.f;
 #pragma unroll
   for (int k = 0; k < NAC; k++) acc = fmaf(h2f(w[k]), xs[k], acc);
-  float tp = a.tproj[row], lp = a.llm[row];
-  a.seq[0 * DIM + row] = acc;
-  a.seq[1 * DIM + row] = tp;
-  a.seq[2 * DIM + row] = lp;
-  a.seq[3 * DIM + row] = acc;
-  a.seq[4 * DIM + row] = tp;
-  a.seq[5 * DIM + row] = 0.f;
+  const float tp = a.tproj[row], lp = a.llm[row];
+  const float y[FMV] = {acc, tp, lp, acc, tp, 0.f};
+  const float g = h2f(a.gn[row]);
+  __shared__ float red[4][FMV];
+#pragma unroll
+  for (int v = 0; v < FMV; v++) {
+    a.seq[v * DIM + row] = y[v];
+    bpack_put(a.Bn, v, row, y[v] * g);
+    const float s2 = wave_sum(y[v] * y[v]);
+    if ((t & 63) == 0) red[t >> 6][v] = s2;
+  }
+  __syncthreads();
+  if (t < FMV) a.ssq_out[blockIdx.x * FMV + t] = red[0][t] + red[1][t] + red[2][t] + red[3][t];
 }
 
 // Bidirectional 3-token GQA attention of both CFG branches: grid (NH, 2),
-// one wave per (head, branch); q [6][QD], k/v [6][KVD], out [6][QD].
+// one wave per (head, branch); q [6][QD], k/v [6][KVD], out [6][QD], and
+// out in the packed form of the O projection's input.
 __global__ __launch_bounds__(64) void fm_attn_kernel(const float *q, const float *k,
-                                                     const float *v, float *out) {
+                                                     const float *v, float *out, h8 *Bn) {
   const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   const int kvh = h / (NH / NKV);
   const float scale = 1.0f / sqrtf((float)HD);
@@ -810,8 +1005,12 @@ __global__ __launch_bounds__(64) void fm_attn_kernel(const float *q, const float
     float sum = e0 + e1 + e2;
     e0 /= sum; e1 /= sum; e2 /= sum;
     const int vec = b * 3 + i;
-    out[(size_t)vec * QD + h * HD + lane * 2] = e0 * vv[0][0] + e1 * vv[1][0] + e2 * vv[2][0];
-    out[(size_t)vec * QD + h * HD + lane * 2 + 1] = e0 * vv[0][1] + e1 * vv[1][1] + e2 * vv[2][1];
+    const float o0 = e0 * vv[0][0] + e1 * vv[1][0] + e2 * vv[2][0];
+    const float o1 = e0 * vv[0][1] + e1 * vv[1][1] + e2 * vv[2][1];
+    out[(size_t)vec * QD + h * HD + lane * 2] = o0;
+    out[(size_t)vec * QD + h * HD + lane * 2 + 1] = o1;
+    bpack_put(Bn, vec, h * HD + lane * 2, o0);
+    bpack_put(Bn, vec, h * HD + lane * 2 + 1, o1);
   }
 }
 
