@@ -113,6 +113,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-frames", action="store_true")
     ap.add_argument("--no-f16-kv", action="store_true", help="skip the f16-KV-cache variant")
+    ap.add_argument("--no-long", action="store_true", help="skip the context-4096 decode")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="also run a plain device copy of this many MB (a known-traffic "
                          "kernel for scaling hardware byte counters)")
@@ -182,6 +183,22 @@ def main():
         log(f"[gpu] frame loop {fms / args.frames * 1000:.1f} us/frame -> {fps:.1f} frames/s "
             f"= {fps * 0.08:.1f}x real-time")
 
+    # ---- long-context decode: 200 steps at positions 3896..4095 over a
+    # synthetic N(0,1) KV cache (values f16-exact), context growing to 4096
+    long_ctx = None
+    if not args.no_long:
+        start, n = 3896, 200
+        eng.fill_kv_synthetic(0, start)
+        eng.position = start
+        eng.time_backbone_steps(5, hold_position=True)
+        lms = eng.time_backbone_steps(n, hold_position=False)
+        lfps = n * 1000.0 / lms
+        lb = step_bytes(start + 1 + (n - 1) / 2.0)
+        long_ctx = {"positions": [start, start + n - 1], "steps": n,
+                    "ms_per_step": round(lms / n, 5), "frames_per_s": round(lfps, 2),
+                    "hbm_frac": round(lb * lfps / 1e9 / HBM_PEAK_GBPS, 4)}
+        log(f"[gpu] context {start}..{start + n}: {lms / n * 1000:.1f} us/step -> {lfps:.1f} frames/s")
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_seconds)
@@ -212,7 +229,8 @@ def main():
                      "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
         "roofline": roofline, "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()}
                                           for k, v in kern.items()},
-        "frame_loop": frame, "f16_kv_variant": f16kv, "cpu_baseline": cpu,
+        "frame_loop": frame, "long_context": long_ctx, "f16_kv_variant": f16kv,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
 

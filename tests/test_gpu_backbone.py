@@ -284,3 +284,31 @@ def test_f16_kv_cache(pair1_f16, pos):
     rows = O.gen_f32(SEED + 5, "kv.rows", 2 * 1024).reshape(2, 1024)
     g.write_kv(0, 1, 1000, rows)
     assert np.array_equal(g.read_kv(0, 1, 1000, 2), rows.astype(np.float16).astype(np.float32))
+
+
+def test_long_context_decode():
+    """Consecutive decode steps near the 4096-slot cap (context 4000..4095):
+    128 keys per attention split, four LDS tiles per block."""
+    g = gpu_engine(n_layers=1, max_seq=4096)
+    o = oracle_engine(n_layers=1, max_seq=4096)
+    try:
+        g.fill_kv_synthetic(SEED, 4000)
+        fill_oracle_kv(o, SEED, 4000)
+        g.position = 4000
+        o.position = 4000
+        for i, pos in enumerate((4000, 4001, 4002)):
+            x = O.gen_f32(SEED + 40 + i, "input.hidden", 3072)
+            _, gn = g.backbone_step(precomputed=x)
+            o.backbone_step(precomputed=x)
+            assert max_rel_err(g.debug_read("attn_out", 4096), o.buffer("attn_out")) < 1e-3
+            assert max_rel_err(gn, o.buffer("normed")) < 1e-3, pos
+        g.position = 4095
+        o.position = 4095
+        x = O.gen_f32(SEED + 50, "input.hidden", 3072)
+        _, gn = g.backbone_step(precomputed=x)
+        o.backbone_step(precomputed=x)
+        assert max_rel_err(gn, o.buffer("normed")) < 1e-3
+        assert g.position == 4096
+    finally:
+        g.destroy()
+        o.close()

@@ -71,6 +71,7 @@ struct vx_engine {
   int *counter = nullptr, *pos = nullptr, *frame = nullptr;
   uint32_t *sem_code = nullptr, *codes = nullptr, *argmax_res = nullptr;
   uint64_t *noise_seed = nullptr;
+  float *inv_freq = nullptr;  // rope inverse frequencies [HD/2]
   float *fm_seq = nullptr, *fm_q = nullptr, *fm_k = nullptr, *fm_v = nullptr, *fm_attn = nullptr,
         *fm_act = nullptr, *fm_llm_out = nullptr, *sem_logits = nullptr, *tproj = nullptr,
         *xh = nullptr, *vel = nullptr, *noise = nullptr, *time_embed = nullptr;
@@ -195,7 +196,7 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
     a.vc = e->vc(l);
     a.kv_f32 = e->kv_f32;
     a.max_seq = e->max_seq;
-    a.theta = e->cfg.rope_theta;
+    a.inv_freq = e->inv_freq;
     launch_gemv1<6, 1, 1, EPI_QKV_ROPE, true, DIM, 1>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_ATTN) {
@@ -667,6 +668,7 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   aplace((void **)&e->vel, (size_t)ns * 2 * NAC * 4);
   aplace((void **)&e->noise, NAC * 4);
   aplace((void **)&e->time_embed, DIM * 4);
+  aplace((void **)&e->inv_freq, HD / 2 * 4);
   aplace((void **)&e->fm_b_attn, (size_t)DIM / 8 * BCOL * 16);
   aplace((void **)&e->fm_b_o, (size_t)QD / 8 * BCOL * 16);
   aplace((void **)&e->fm_b_ffn, (size_t)DIM / 8 * BCOL * 16);
@@ -679,6 +681,12 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   }
   for (auto &o : aoffs) *o.first = (char *)e->aarena + o.second;
   (void)hipMemsetAsync(e->aarena, 0, abytes, e->st);
+  // rope frequencies, src/shaders.ts:224-256: freq_i = 1 / theta^(2i/128), evaluated once
+  // here in f32 (the shader evaluates the same expression per element)
+  float inv_freq[HD / 2];
+  for (int i = 0; i < HD / 2; i++)
+    inv_freq[i] = 1.0f / powf(cfg.rope_theta, (float)(i * 2) / (float)HD);
+  (void)hipMemcpyAsync(e->inv_freq, inv_freq, sizeof inv_freq, hipMemcpyHostToDevice, e->st);
   if (hipStreamSynchronize(e->st) != hipSuccess) {
     vx_destroy(e);
     return fail(nullptr, VX_E_DEVICE, "device initialisation failed");

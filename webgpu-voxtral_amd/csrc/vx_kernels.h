@@ -37,6 +37,7 @@ constexpr int QKV_ROWS = QD + 2 * KVD;  // 6144
 constexpr int NAC = 36;
 constexpr int SEMV = 8320;
 constexpr int ATTN_SPLITS = 32;  // split-K factor of the decode attention
+static_assert(ATTN_SPLITS <= 64 && (ATTN_SPLITS & (ATTN_SPLITS - 1)) == 0, "splits: power of 2, <= 64");
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -128,7 +129,7 @@ struct GemvArgs {
   void *kc, *vc;  // this layer's K and V cache [NKV][max_seq][HD], f32 or f16
   int kv_f32;     // 1: f32 cache elements (the reference's), 0: f16
   int max_seq;
-  float theta;
+  const float *inv_freq;  // rope: 1 / theta^(2i/HD), i < HD/2
 };
 
 // one K/V cache element pair (d, d+1) of head row `row` at position pos
@@ -328,7 +329,7 @@ __device__ __forceinline__ void unit_epilogue(const GemvArgs &a, int unit, const
     const float y0 = y[0], y1 = y[1];
     if (row < QD + KVD) {
       const int pair = (row & (HD - 1)) >> 1;
-      const float freq = 1.0f / powf(a.theta, (float)(pair * 2) / (float)HD);
+      const float freq = a.inv_freq[pair];
       const float ang = (float)pos * freq;
       const float cs = cosf(ang), sn = sinf(ang);
       const float r0 = y0 * cs - y1 * sn, r1 = y0 * sn + y1 * cs;
@@ -573,24 +574,26 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
 
 // Combine: one wave per query head.  M = max m_s, L = sum l_s e^(m_s - M),
 // o = sum o_s e^(m_s - M) / L (splits without keys carry m = -inf, l = 0).
+// Every load of the head (m, l of each split, both output dims of each
+// split) is issued before the first is used: one memory round trip.
 __global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, float *out) {
   const int h = blockIdx.x, lane = threadIdx.x;
   const float *hp = part + (size_t)h * ATTN_SPLITS * (HD + 2);
-  float ms = -INFINITY, ls = 0.f;
-  if (lane < ATTN_SPLITS) {
-    ms = hp[lane * (HD + 2) + HD];
-    ls = hp[lane * (HD + 2) + HD + 1];
-  }
+  const float *mlp = hp + (lane & (ATTN_SPLITS - 1)) * (HD + 2) + HD;
+  const float mv = mlp[0], lv = mlp[1];
+  float2 o[ATTN_SPLITS];
+#pragma unroll
+  for (int s = 0; s < ATTN_SPLITS; s++) o[s] = *(const float2 *)(hp + s * (HD + 2) + lane * 2);
+  const float ms = lane < ATTN_SPLITS ? mv : -INFINITY;
   const float M = wave_max(ms);
-  const float wgt = (lane < ATTN_SPLITS) ? expf(ms - M) : 0.f;
-  const float L = wave_sum(ls * wgt);
+  const float wgt = lane < ATTN_SPLITS ? expf(ms - M) : 0.f;
+  const float L = wave_sum(lane < ATTN_SPLITS ? lv * wgt : 0.f);
   float r0 = 0.f, r1 = 0.f;
-#pragma unroll 8
+#pragma unroll
   for (int s = 0; s < ATTN_SPLITS; s++) {
     const float ws = __shfl(wgt, s, 64);
-    const float *op = hp + s * (HD + 2) + lane * 2;
-    r0 = fmaf(ws, op[0], r0);
-    r1 = fmaf(ws, op[1], r1);
+    r0 = fmaf(ws, o[s].x, r0);
+    r1 = fmaf(ws, o[s].y, r1);
   }
   out[h * HD + lane * 2] = r0 / L;
   out[h * HD + lane * 2 + 1] = r1 / L;
