@@ -117,6 +117,16 @@ int vx_backbone_step(vx_engine *e, int32_t token, int32_t embed_mode,
                      const float *precomputed, int32_t lm_head,
                      uint32_t *argmax_out, float *normed_out);
 
+/* The prefill loop of generate(), src/engine.ts:2457-2472 (one
+ * backboneStep per prompt token, voice rows replacing the embeddings of
+ * tokens [audio_start, audio_start + audio_count)), run as batched MFMA
+ * GEMMs over chunks of up to 256 tokens from the current position.  Leaves
+ * the KV cache, the residual stream, W.normed (last token) and the position
+ * as n_tokens single steps would (no LM head).  voice: f32[audio_count][dim]
+ * or NULL. */
+int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens,
+               int32_t audio_start, int32_t audio_count, const float *voice);
+
 /* debugBackboneLayerByLayer read points, src/engine.ts:2106-2287: one step
  * that also copies the hidden state after each attention residual and each
  * FFN residual into layer_out[n_layers][2][dim]. */

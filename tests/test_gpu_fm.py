@@ -80,18 +80,22 @@ def test_velocity_history(pair):
 
 
 def test_many_frames_codes_identical(pair):
-    """Teacher-forced frames: FSQ codes identical on >= 99% of frames."""
+    """Teacher-forced frames (both sides get the same backbone output and
+    noise): all 36 FSQ codes identical on >= 99% of 100 frames, and x_t
+    within the hidden-state bar on every frame."""
     g, o = pair
-    n = 12
-    same = 0
+    n = 100
+    same, worst = 0, 0.0
     for f in range(n):
         normed = O.gen_f32(SEED + 100 + f, "fm.normed", 3072)
         noise = O.gen_f32(SEED + 100 + f, "fm.noise.test", 36)
         out = run_frame(g, o, normed, noise)
         same += int(np.array_equal(out["acoustic_codes"], o.acoustic_codes))
-        assert max_rel_err(out["x_final"], o.buffer("x_t")) < 1e-2
-    print(f"{same}/{n} frames with identical codes")
-    assert same >= n - 1 if n < 100 else same >= 0.99 * n
+        err = max_rel_err(out["x_final"], o.buffer("x_t"))
+        worst = max(worst, err)
+        assert err < 1e-2, (f, err)
+    print(f"{same}/{n} frames with identical codes, worst x_t error {worst:.2e}")
+    assert same >= 0.99 * n
 
 
 def test_device_noise_generator(pair):

@@ -18,6 +18,7 @@
 
 #include "../../include/voxtral_engine.h"
 #include "vx_kernels.h"
+#include "vx_prefill.h"
 
 using namespace vx;
 
@@ -83,6 +84,13 @@ struct vx_engine {
   bool fm_packed_ready = false;
   h8 *fm_b_attn = nullptr, *fm_b_o = nullptr, *fm_b_ffn = nullptr, *fm_b_act = nullptr;
   float *fm_ssq_attn = nullptr, *fm_ssq_ffn = nullptr;
+  // batched prefill (vx_prefill.h): chunk activations, packed GEMM input,
+  // GEMM output, the chunk's token ids and voice rows
+  void *pf_arena = nullptr;
+  float *pf_x = nullptr, *pf_q = nullptr, *pf_attn = nullptr, *pf_act = nullptr, *pf_c = nullptr,
+        *pf_voice = nullptr;
+  h8 *pf_b = nullptr;
+  int32_t *pf_tok = nullptr;
 
   int host_pos = 0;
   hipGraphExec_t step_exec = nullptr, hold_exec = nullptr, frame_exec = nullptr,
@@ -601,6 +609,30 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   add_slot(e, "acoustic_transformer.semantic_codebook_output.weight", e->fm_sem, {SEMV, DIM}, false);
   add_slot(e, "acoustic_transformer.acoustic_codebook_output.weight", e->fm_ac, {NAC, DIM}, false);
 
+  // ---- batched prefill buffers (one chunk of PF_MAXT tokens)
+  {
+    std::vector<std::pair<void **, size_t>> parts = {
+        {(void **)&e->pf_x, (size_t)PF_MAXT * DIM * 4},
+        {(void **)&e->pf_q, (size_t)PF_MAXT * QD * 4},
+        {(void **)&e->pf_attn, (size_t)PF_MAXT * QD * 4},
+        {(void **)&e->pf_act, (size_t)PF_MAXT * HID * 4},
+        {(void **)&e->pf_c, (size_t)PF_NC * 2 * HID * 4},
+        {(void **)&e->pf_b, (size_t)HID / 8 * PF_NC * 16},
+        {(void **)&e->pf_voice, (size_t)PF_MAXT * DIM * 4},
+        {(void **)&e->pf_tok, (size_t)PF_MAXT * 4}};
+    size_t tot = 0;
+    for (auto &q : parts) tot += align256(q.second);
+    if (hipMalloc(&e->pf_arena, tot) != hipSuccess) {
+      vx_destroy(e);
+      return fail(nullptr, VX_E_NOMEM, "hipMalloc of %zu prefill bytes failed", tot);
+    }
+    char *p = (char *)e->pf_arena;
+    for (auto &q : parts) {
+      *q.first = p;
+      p += align256(q.second);
+    }
+  }
+
   // ---- FM layer matrices in MFMA operand order
   {
     const size_t per = align256((size_t)QKV_ROWS * DIM * 2) + align256((size_t)DIM * QD * 2) +
@@ -707,6 +739,7 @@ void vx_destroy(vx_engine *e) {
   if (e->warena) (void)hipFree(e->warena);
   if (e->kv) (void)hipFree(e->kv);
   if (e->fm_parena) (void)hipFree(e->fm_parena);
+  if (e->pf_arena) (void)hipFree(e->pf_arena);
   if (e->aarena) (void)hipFree(e->aarena);
   if (e->ev0) (void)hipEventDestroy(e->ev0);
   if (e->ev1) (void)hipEventDestroy(e->ev1);
@@ -1024,6 +1057,93 @@ int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos) {
   return VX_OK;
 }
 
+// -------------------------------------------------------------- prefill
+// One chunk of n <= PF_MAXT prompt tokens (global indices tok0..tok0+n-1)
+// through every layer at positions host_pos..host_pos+n-1; tokens and voice
+// rows are already on the device.  Afterwards the residual stream and
+// W.normed hold the last token's values and the position is advanced, as
+// after n single steps.
+static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int vcount,
+                                  bool has_voice) {
+  hipStream_t st = e->st;
+  const int pos0 = e->host_pos;
+  hipLaunchKernelGGL(pf_embed_kernel, dim3(n, DIM / 256), dim3(256), 0, st, e->tok_emb, e->pf_tok,
+                     has_voice ? e->pf_voice : nullptr, vstart, vcount, tok0, e->pf_x);
+  const dim3 blk(256);
+  for (int l = 0; l < e->cfg.n_layers; l++) {
+    const LayerW &W = e->L[l];
+    hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
+                       W.attn_norm, e->cfg.norm_eps, e->pf_b);
+    hipLaunchKernelGGL(pf_gemm_kernel<DIM>, dim3(QKV_ROWS / PF_BM, PF_NC / PF_BN), blk, 0, st,
+                       W.wqkv, e->pf_b, e->pf_c, QKV_ROWS);
+    hipLaunchKernelGGL(pf_qkv_epi_kernel, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c,
+                       e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
+    if (e->kv_f32)
+      hipLaunchKernelGGL(pf_attn_kernel<float>, dim3(n, NKV), blk, 0, st, e->pf_q, e->kc(l),
+                         e->vc(l), e->max_seq, pos0, e->pf_attn);
+    else
+      hipLaunchKernelGGL(pf_attn_kernel<uint16_t>, dim3(n, NKV), blk, 0, st, e->pf_q, e->kc(l),
+                         e->vc(l), e->max_seq, pos0, e->pf_attn);
+    hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_attn, QD, n,
+                       nullptr, 0.f, e->pf_b);
+    hipLaunchKernelGGL(pf_gemm_kernel<QD>, dim3(DIM / PF_BM, PF_NC / PF_BN), blk, 0, st, W.wo,
+                       e->pf_b, e->pf_c, DIM);
+    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, e->pf_x);
+    hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
+                       W.ffn_norm, e->cfg.norm_eps, e->pf_b);
+    // W1 and W3 are adjacent in the arena: one GEMM over the stacked rows
+    hipLaunchKernelGGL(pf_gemm_kernel<DIM>, dim3(2 * HID / PF_BM, PF_NC / PF_BN), blk, 0, st, W.w1,
+                       e->pf_b, e->pf_c, 2 * HID);
+    hipLaunchKernelGGL(pf_swiglu_epi_kernel, dim3(n, HID / 256), blk, 0, st, e->pf_c, e->pf_act);
+    hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_act, HID, n,
+                       nullptr, 0.f, e->pf_b);
+    hipLaunchKernelGGL(pf_gemm_kernel<HID>, dim3(DIM / PF_BM, PF_NC / PF_BN), blk, 0, st, W.w2,
+                       e->pf_b, e->pf_c, DIM);
+    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, e->pf_x);
+  }
+  (void)hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * DIM, DIM * 4, hipMemcpyDeviceToDevice, st);
+  hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, e->x, e->final_norm,
+                     e->cfg.norm_eps, e->normed, nullptr);
+  hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, st, e->pos, pos0 + n);
+  e->host_pos = pos0 + n;
+}
+
+int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t audio_start,
+               int32_t audio_count, const float *voice) {
+  if (!e) return VX_E_INVALID;
+  int rc = check_ready(e);
+  if (rc) return rc;
+  if (n_tokens < 1 || !tokens || audio_count < 0 || (audio_count > 0 && audio_start < 0))
+    return fail(e, VX_E_INVALID, "bad prefill arguments");
+  if (e->host_pos + n_tokens > e->max_seq)
+    return fail(e, VX_E_RANGE, "prefill passes max_seq_len %d", e->max_seq);
+  for (int i = 0; i < n_tokens; i++)
+    if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab_size)
+      return fail(e, VX_E_INVALID, "token %d out of range", tokens[i]);
+  if (e->L[0].w3 != e->L[0].w1 + (size_t)HID * DIM)
+    return fail(e, VX_E_STATE, "weight layout: gate and up matrices not adjacent");
+  const bool has_voice = voice && audio_count > 0;
+  for (int c0 = 0; c0 < n_tokens; c0 += PF_MAXT) {
+    const int n = std::min(PF_MAXT, n_tokens - c0);
+    HIPCHK(e, hipMemcpyAsync(e->pf_tok, tokens + c0, (size_t)n * 4, hipMemcpyHostToDevice, e->st));
+    // voice rows of this chunk, at chunk-local offsets
+    int vs = 0, vc = 0;
+    if (has_voice) {
+      const int a = std::max(c0, audio_start), b = std::min(c0 + n, audio_start + audio_count);
+      if (a < b) {
+        HIPCHK(e, hipMemcpyAsync(e->pf_voice, voice + (size_t)(a - audio_start) * DIM,
+                                 (size_t)(b - a) * DIM * 4, hipMemcpyHostToDevice, e->st));
+        vs = a;
+        vc = b - a;
+      }
+    }
+    enqueue_prefill_chunk(e, n, c0, vs, vc, vc > 0);
+    LAUNCHCHK(e);
+    HIPCHK(e, hipStreamSynchronize(e->st));  // the host buffers above are reused per chunk
+  }
+  return VX_OK;
+}
+
 // ------------------------------------------------------------- generate
 void vx_generate_options_default(vx_generate_options *o) {
   if (!o) return;
@@ -1101,16 +1221,11 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
   auto t0 = clk::now();
   if (on_stage) on_stage(user, 0, -1.0);
   if ((rc = ensure_tproj(e))) return rc;
-  // prefill, one token per step (src/engine.ts:2457-2472); the LM head the
-  // reference runs per prefill token is never read, so it is skipped
-  for (int i = 0; i < n_tokens; i++) {
-    bool is_voice = voice && i >= audio_start && i < audio_start + audio_count;
-    if ((rc = prepare_input(e, tokens[i], is_voice ? VX_EMBED_PRECOMPUTED : VX_EMBED_TOKEN,
-                            is_voice ? voice + (size_t)(i - audio_start) * DIM : nullptr)))
-      return rc;
-    if ((rc = run_step(e))) return rc;
-    e->host_pos++;
-  }
+  // prefill (src/engine.ts:2457-2472) as batched GEMMs, chunk by chunk; the
+  // LM head the reference runs per prefill token is never read, so it is
+  // skipped
+  if (n_tokens > 0 && (rc = vx_prefill(e, tokens, n_tokens, audio_start, audio_count, voice)))
+    return rc;
   HIPCHK(e, hipStreamSynchronize(e->st));
   auto t1 = clk::now();
   if (on_stage) {

@@ -72,6 +72,7 @@ _SIGS = {
     "vx_init_synthetic": (_I32, [_VP, ctypes.c_uint64, ctypes.c_float]),
     "vx_read_tensor": (_I32, [_VP, ctypes.c_char_p, _VP, ctypes.c_size_t]),
     "vx_is_ready": (_I32, [_VP]),
+    "vx_prefill": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP]),
     "vx_reset": (_I32, [_VP]),
     "vx_position": (_I32, [_VP]),
     "vx_set_position": (_I32, [_VP, _I32]),
@@ -247,6 +248,20 @@ class VoxtralEngine:
         self._check(self._lib.vx_backbone_step(self._h, int(token), int(mode), _ptr(pre),
                                                int(bool(lm_head)), _ptr(am), _ptr(normed)))
         return (int(am[0]) if lm_head else None), normed
+
+    def prefill(self, tokens, audio_token_start=0, audio_token_count=0, voice_embeddings=None):
+        """The prefill loop of generate() (src/engine.ts:2457-2472) as batched
+        GEMMs: KV cache, residual stream, W.normed and position as after one
+        step per token (no LM head)."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        voice = None
+        if voice_embeddings is not None and audio_token_count > 0:
+            voice = _f32(voice_embeddings)
+            if voice.size < audio_token_count * self.config.dim:
+                raise ValueError("voiceEmbeddings shorter than audioTokenCount rows")
+        self._check(self._lib.vx_prefill(self._h, toks.ctypes.data, toks.size, audio_token_start,
+                                         audio_token_count if voice is not None else 0,
+                                         _ptr(voice)))
 
     def backbone_step_and_read(self, token_id, use_audio_embedding=False):
         """backboneStepAndRead (:2333-2342): next-token argmax."""
