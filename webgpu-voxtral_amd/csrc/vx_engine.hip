@@ -1063,6 +1063,14 @@ int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos) {
 // rows are already on the device.  Afterwards the residual stream and
 // W.normed hold the last token's values and the position is advanced, as
 // after n single steps.
+// k splits of the narrow prefill GEMMs (grid >= 192 blocks; the split
+// slabs fit the GEMM output buffer of the stacked gate/up GEMM)
+constexpr int PF_S_QKV = 3, PF_S_O = 4, PF_S_DOWN = 6;
+static_assert(PF_S_QKV * QKV_ROWS <= 2 * HID && PF_S_O * DIM <= 2 * HID &&
+                  PF_S_DOWN * DIM <= 2 * HID && (DIM / 32) % PF_S_QKV == 0 &&
+                  (QD / 32) % PF_S_O == 0 && (HID / 32) % PF_S_DOWN == 0,
+              "prefill k splits");
+
 static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int vcount,
                                   bool has_voice) {
   hipStream_t st = e->st;
@@ -1074,10 +1082,11 @@ static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int
     const LayerW &W = e->L[l];
     hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
                        W.attn_norm, e->cfg.norm_eps, e->pf_b);
-    hipLaunchKernelGGL(pf_gemm_kernel<DIM>, dim3(QKV_ROWS / PF_BM, PF_NC / PF_BN), blk, 0, st,
-                       W.wqkv, e->pf_b, e->pf_c, QKV_ROWS);
+    hipLaunchKernelGGL(pf_gemm_kernel<DIM>, dim3(QKV_ROWS / PF_BM, PF_NC / PF_BN, PF_S_QKV), blk, 0,
+                       st, W.wqkv, e->pf_b, e->pf_c, QKV_ROWS);
     hipLaunchKernelGGL(pf_qkv_epi_kernel, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c,
-                       e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
+                       PF_S_QKV, e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0,
+                       e->inv_freq);
     if (e->kv_f32)
       hipLaunchKernelGGL(pf_attn_kernel<float>, dim3(n, NKV), blk, 0, st, e->pf_q, e->kc(l),
                          e->vc(l), e->max_seq, pos0, e->pf_attn);
@@ -1086,9 +1095,10 @@ static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int
                          e->vc(l), e->max_seq, pos0, e->pf_attn);
     hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_attn, QD, n,
                        nullptr, 0.f, e->pf_b);
-    hipLaunchKernelGGL(pf_gemm_kernel<QD>, dim3(DIM / PF_BM, PF_NC / PF_BN), blk, 0, st, W.wo,
-                       e->pf_b, e->pf_c, DIM);
-    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, e->pf_x);
+    hipLaunchKernelGGL(pf_gemm_kernel<QD>, dim3(DIM / PF_BM, PF_NC / PF_BN, PF_S_O), blk, 0, st,
+                       W.wo, e->pf_b, e->pf_c, DIM);
+    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, PF_S_O,
+                       e->pf_x);
     hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
                        W.ffn_norm, e->cfg.norm_eps, e->pf_b);
     // W1 and W3 are adjacent in the arena: one GEMM over the stacked rows
@@ -1097,9 +1107,10 @@ static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int
     hipLaunchKernelGGL(pf_swiglu_epi_kernel, dim3(n, HID / 256), blk, 0, st, e->pf_c, e->pf_act);
     hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_act, HID, n,
                        nullptr, 0.f, e->pf_b);
-    hipLaunchKernelGGL(pf_gemm_kernel<HID>, dim3(DIM / PF_BM, PF_NC / PF_BN), blk, 0, st, W.w2,
-                       e->pf_b, e->pf_c, DIM);
-    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, e->pf_x);
+    hipLaunchKernelGGL(pf_gemm_kernel<HID>, dim3(DIM / PF_BM, PF_NC / PF_BN, PF_S_DOWN), blk, 0, st,
+                       W.w2, e->pf_b, e->pf_c, DIM);
+    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM,
+                       PF_S_DOWN, e->pf_x);
   }
   (void)hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * DIM, DIM * 4, hipMemcpyDeviceToDevice, st);
   hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, e->x, e->final_norm,
