@@ -173,13 +173,17 @@ int vx_read_kv(vx_engine *e, int32_t layer, int32_t which, int32_t pos0,
 int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos);
 
 /* ----------------------------------------------------------- generate() */
-#define VX_SAMPLE_TOP_P 0  /* reference: masked top-p 0.9, T 0.8 on host */
-#define VX_SAMPLE_GREEDY 1 /* masked argmax on the device, no readback */
+/* Semantic-code sampling of generate() (src/engine.ts:2556-2567): the
+ * logits masked (index 0, indices >= 8194), then sampleTopP(0.9, 0.8)
+ * (src/engine.ts:247-289) with a seeded uniform instead of Math.random. */
+#define VX_SAMPLE_TOP_P 0      /* top-p on the device: no logits readback */
+#define VX_SAMPLE_GREEDY 1     /* masked argmax on the device */
+#define VX_SAMPLE_TOP_P_HOST 2 /* the same top-p on the host (logits read back) */
 
 typedef struct vx_generate_options {
   int32_t sampling;   /* VX_SAMPLE_* */
-  float top_p;        /* 0.9 */
-  float temperature;  /* 0.8 */
+  double top_p;       /* 0.9 (a JS number in the reference) */
+  double temperature; /* 0.8 */
   uint64_t seed;      /* noise + sampling seed (reference: Math.random) */
   int32_t ignore_eos; /* 1: run exactly max_frames (benchmarks) */
 } vx_generate_options;
@@ -211,6 +215,14 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens,
                 vx_frame_cb on_frame, vx_stage_cb on_stage, void *user,
                 uint32_t *semantic_out, uint32_t *acoustic_out,
                 vx_generate_stats *stats);
+
+/* sampleTopP on caller logits (test plumbing): logits f32[n] with indices
+ * 0 and >= valid masked, n <= 16384.  *state: the splitmix64 state of the
+ * uniform (advanced by one draw).  on_device != 0 runs the device kernel
+ * used by generate(), else the host implementation. */
+int vx_sample_top_p(vx_engine *e, const float *logits, int32_t n, int32_t valid,
+                    double top_p, double temperature, uint64_t *state,
+                    int32_t on_device, uint32_t *code);
 
 /* ------------------------------------------------------ measurement */
 /* No reference counterparts (the reference times on the CPU,

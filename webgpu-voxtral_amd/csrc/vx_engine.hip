@@ -97,6 +97,14 @@ struct vx_engine {
                  fm_greedy_exec = nullptr, fm_plain_exec = nullptr;
   bool use_graphs = true;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // device top-p: its uniform stream and (top_p, temperature); a logits
+  // buffer for vx_sample_top_p; pinned per-frame readback slots
+  uint64_t *rng_state = nullptr;
+  double *tp_params = nullptr;
+  float *tp_logits = nullptr;
+  uint32_t *h_frame = nullptr;  // [2][1 + NAC]
+  hipEvent_t ev_frame[2] = {nullptr, nullptr};
+  hipGraphExec_t fm_topp_exec = nullptr, frame_topp_exec = nullptr;
 
   void *kc(int l) const { return (char *)kv + (size_t)(2 * l) * NKV * max_seq * HD * kv_elem; }
   void *vc(int l) const { return (char *)kv + (size_t)(2 * l + 1) * NKV * max_seq * HD * kv_elem; }
@@ -392,11 +400,23 @@ static void fm_plain_body(vx_engine *e) {
                      kNoiseStream, e->frame);
   enqueue_fm(e, e->noise, false);
 }
+// FM, then the semantic code by device top-p (masked, src/engine.ts:2556-2567)
+static void fm_topp_body(vx_engine *e) {
+  fm_plain_body(e);
+  hipLaunchKernelGGL(topp_sample_kernel, dim3(1), dim3(TP_NT), 0, e->st, e->sem_logits, SEMV, 8194,
+                     e->tp_params, e->rng_state, e->sem_code);
+}
 static void frame_body(vx_engine *e) {
   hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
                      e->sem_code, e->codes, e->x);
   enqueue_backbone(e);
   fm_greedy_body(e);
+}
+static void frame_topp_body(vx_engine *e) {
+  hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
+                     e->sem_code, e->codes, e->x);
+  enqueue_backbone(e);
+  fm_topp_body(e);
 }
 
 // Runs one captured sequence: replays its hipGraph (captured on first use),
@@ -533,6 +553,12 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   }
   (void)hipEventCreate(&e->ev0);
   (void)hipEventCreate(&e->ev1);
+  (void)hipEventCreateWithFlags(&e->ev_frame[0], hipEventDisableTiming);
+  (void)hipEventCreateWithFlags(&e->ev_frame[1], hipEventDisableTiming);
+  if (hipHostMalloc((void **)&e->h_frame, 2 * (1 + NAC) * 4, hipHostMallocDefault) != hipSuccess) {
+    vx_destroy(e);
+    return fail(nullptr, VX_E_NOMEM, "hipHostMalloc of readback slots failed");
+  }
 
   // ---- weight table (names: src/engine.ts:659-743)
   struct Req {
@@ -687,6 +713,9 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   aplace((void **)&e->codes, 64 * 4);
   aplace((void **)&e->argmax_res, 4);
   aplace((void **)&e->noise_seed, 8);
+  aplace((void **)&e->rng_state, 8);
+  aplace((void **)&e->tp_params, 16);
+  aplace((void **)&e->tp_logits, (size_t)TP_N * 4);
   aplace((void **)&e->fm_seq, 6 * DIM * 4);
   aplace((void **)&e->fm_q, 6 * QD * 4);
   aplace((void **)&e->fm_k, 6 * KVD * 4);
@@ -734,6 +763,11 @@ void vx_destroy(vx_engine *e) {
   if (e->step_exec) (void)hipGraphExecDestroy(e->step_exec);
   if (e->hold_exec) (void)hipGraphExecDestroy(e->hold_exec);
   if (e->fm_greedy_exec) (void)hipGraphExecDestroy(e->fm_greedy_exec);
+  if (e->fm_topp_exec) (void)hipGraphExecDestroy(e->fm_topp_exec);
+  if (e->frame_topp_exec) (void)hipGraphExecDestroy(e->frame_topp_exec);
+  for (auto &ev : e->ev_frame)
+    if (ev) (void)hipEventDestroy(ev);
+  if (e->h_frame) (void)hipHostFree(e->h_frame);
   if (e->fm_plain_exec) (void)hipGraphExecDestroy(e->fm_plain_exec);
   if (e->frame_exec) (void)hipGraphExecDestroy(e->frame_exec);
   if (e->warena) (void)hipFree(e->warena);
@@ -1155,22 +1189,12 @@ int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t au
   return VX_OK;
 }
 
-// ------------------------------------------------------------- generate
-void vx_generate_options_default(vx_generate_options *o) {
-  if (!o) return;
-  o->sampling = VX_SAMPLE_TOP_P;
-  o->top_p = 0.9f;
-  o->temperature = 0.8f;
-  o->seed = 0;
-  o->ignore_eos = 0;
-}
-
-// sampleTopP, src/engine.ts:247-289, with a seeded uniform in place of
-// Math.random.  Float32Array intermediates, double accumulators, stable
-// descending sort, as the TypeScript does.
-static uint32_t sample_top_p(const float *logits, int n, float top_p, float temp, uint64_t *rng) {
+// sampleTopP, src/engine.ts:247-289 (JS numbers are f64, the arrays f32);
+// Math.random replaced by the next draw of a seeded splitmix64 stream
+static uint32_t sample_top_p(const float *logits, int n, double top_p, double temp,
+                             uint64_t *rng) {
   std::vector<float> sc(n);
-  for (int i = 0; i < n; i++) sc[i] = (float)((double)logits[i] / (double)temp);
+  for (int i = 0; i < n; i++) sc[i] = (float)((double)logits[i] / temp);
   double mx = -INFINITY;
   for (int i = 0; i < n; i++)
     if (sc[i] > mx) mx = sc[i];
@@ -1208,6 +1232,44 @@ static uint32_t sample_top_p(const float *logits, int n, float top_p, float temp
   return (uint32_t)idx[0];
 }
 
+int vx_sample_top_p(vx_engine *e, const float *logits, int32_t n, int32_t valid, double top_p,
+                    double temperature, uint64_t *state, int32_t on_device, uint32_t *code) {
+  if (!e || !logits || !state || !code) return VX_E_INVALID;
+  if (n < 2 || n > TP_N || valid < 2 || temperature <= 0.0)
+    return fail(e, VX_E_INVALID, "top-p: n %d, valid %d out of range", n, valid);
+  if (!on_device) {
+    std::vector<float> l(logits, logits + n);
+    l[0] = -INFINITY;
+    for (int i = valid; i < n; i++) l[i] = -INFINITY;
+    *code = sample_top_p(l.data(), n, top_p, temperature, state);
+    return VX_OK;
+  }
+  const double params[2] = {top_p, temperature};
+  HIPCHK(e, hipMemcpyAsync(e->tp_logits, logits, (size_t)n * 4, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipMemcpyAsync(e->tp_params, params, 16, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipMemcpyAsync(e->rng_state, state, 8, hipMemcpyHostToDevice, e->st));
+  hipLaunchKernelGGL(topp_sample_kernel, dim3(1), dim3(TP_NT), 0, e->st, e->tp_logits, n, valid,
+                     e->tp_params, e->rng_state, e->argmax_res);
+  LAUNCHCHK(e);
+  HIPCHK(e, hipMemcpyAsync(code, e->argmax_res, 4, hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipMemcpyAsync(state, e->rng_state, 8, hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+// ------------------------------------------------------------- generate
+void vx_generate_options_default(vx_generate_options *o) {
+  if (!o) return;
+  o->sampling = VX_SAMPLE_TOP_P;
+  o->top_p = 0.9;
+  o->temperature = 0.8;
+  o->seed = 0;
+  o->ignore_eos = 0;
+}
+
+// sampleTopP, src/engine.ts:247-289, with a seeded uniform in place of
+// Math.random.  Float32Array intermediates, double accumulators, stable
+// descending sort, as the TypeScript does.
 int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t audio_start,
                 int32_t audio_count, const float *voice, int32_t max_frames,
                 const vx_generate_options *opt_in, vx_frame_cb on_frame, vx_stage_cb on_stage,
@@ -1249,41 +1311,81 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
   e->host_pos++;
 
   uint64_t rng = opt.seed ^ 0x5bd1e9955bd1e995ull;
-  std::vector<float> logits(SEMV);
-  uint32_t codes[NAC];
+  const double params[2] = {opt.top_p, opt.temperature};
+  HIPCHK(e, hipMemcpyAsync(e->rng_state, &rng, 8, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipMemcpyAsync(e->tp_params, params, 16, hipMemcpyHostToDevice, e->st));
   int frames = 0;
-  for (int f = 0; f < max_frames; f++) {
-    if (f > 0) {
-      if ((rc = prepare_input(e, 0, VX_EMBED_CODES, nullptr))) return rc;
-      if ((rc = run_step(e))) return rc;
-      e->host_pos++;
-    }
-    const bool greedy = opt.sampling == VX_SAMPLE_GREEDY;
-    rc = greedy ? run_seq(e, &e->fm_greedy_exec, fm_greedy_body)
-                : run_seq(e, &e->fm_plain_exec, fm_plain_body);
-    if (rc) return rc;
-    uint32_t code;
-    if (greedy) {
-      HIPCHK(e, hipMemcpyAsync(&code, e->sem_code, 4, hipMemcpyDeviceToHost, e->st));
-      HIPCHK(e, hipStreamSynchronize(e->st));
-    } else {
+  if (opt.sampling == VX_SAMPLE_TOP_P_HOST) {
+    // the reference's dataflow: logits to the host every frame
+    std::vector<float> logits(SEMV);
+    uint32_t codes[NAC];
+    for (int f = 0; f < max_frames; f++) {
+      if (f > 0) {
+        if ((rc = prepare_input(e, 0, VX_EMBED_CODES, nullptr))) return rc;
+        if ((rc = run_step(e))) return rc;
+        e->host_pos++;
+      }
+      if ((rc = run_seq(e, &e->fm_plain_exec, fm_plain_body))) return rc;
       HIPCHK(e, hipMemcpyAsync(logits.data(), e->sem_logits, SEMV * 4, hipMemcpyDeviceToHost, e->st));
       HIPCHK(e, hipStreamSynchronize(e->st));
       logits[0] = -INFINITY;  // src/engine.ts:2559-2563
       for (int i = 8194; i < SEMV; i++) logits[i] = -INFINITY;
-      code = sample_top_p(logits.data(), SEMV, opt.top_p, opt.temperature, &rng);
-    }
-    if (code <= 1 && !opt.ignore_eos) break;
-    if (!greedy) {
+      const uint32_t code = sample_top_p(logits.data(), SEMV, opt.top_p, opt.temperature, &rng);
+      if (code <= 1 && !opt.ignore_eos) break;
       hipLaunchKernelGGL(set_u32_kernel, dim3(1), dim3(1), 0, e->st, e->sem_code, code);
       LAUNCHCHK(e);
+      HIPCHK(e, hipMemcpyAsync(codes, e->codes, NAC * 4, hipMemcpyDeviceToHost, e->st));
+      HIPCHK(e, hipStreamSynchronize(e->st));
+      if (sem_out) sem_out[f] = code;
+      if (ac_out) memcpy(ac_out + (size_t)f * NAC, codes, sizeof codes);
+      frames++;
+      if (on_frame) on_frame(user, f, code, codes);
     }
-    HIPCHK(e, hipMemcpyAsync(codes, e->codes, NAC * 4, hipMemcpyDeviceToHost, e->st));
-    HIPCHK(e, hipStreamSynchronize(e->st));
-    if (sem_out) sem_out[f] = code;
-    if (ac_out) memcpy(ac_out + (size_t)f * NAC, codes, sizeof codes);
-    frames++;
-    if (on_frame) on_frame(user, f, code, codes);
+  } else {
+    // codes stay on the device: frame f + 1 (multi-codebook embed of frame
+    // f's codes, backbone step, FM, sampling) is enqueued before frame f's
+    // codes are read back through pinned memory, so the host work of frame
+    // f (EOS test, callback) overlaps frame f + 1 on the GPU.  If frame f
+    // ends the utterance, frame f + 1 is discarded: its KV row lies past the
+    // position the engine is left at and is never read.
+    const bool greedy = opt.sampling == VX_SAMPLE_GREEDY;
+    hipGraphExec_t *fm_slot = greedy ? &e->fm_greedy_exec : &e->fm_topp_exec;
+    hipGraphExec_t *frame_slot = greedy ? &e->frame_exec : &e->frame_topp_exec;
+    void (*fm_body)(vx_engine *) = greedy ? fm_greedy_body : fm_topp_body;
+    void (*fr_body)(vx_engine *) = greedy ? frame_body : frame_topp_body;
+    auto enqueue_frame = [&](int f) -> int {
+      int r = f == 0 ? run_seq(e, fm_slot, fm_body) : run_seq(e, frame_slot, fr_body);
+      if (r) return r;
+      uint32_t *slot = e->h_frame + (f & 1) * (1 + NAC);
+      HIPCHK(e, hipMemcpyAsync(slot, e->sem_code, 4, hipMemcpyDeviceToHost, e->st));
+      HIPCHK(e, hipMemcpyAsync(slot + 1, e->codes, NAC * 4, hipMemcpyDeviceToHost, e->st));
+      HIPCHK(e, hipEventRecord(e->ev_frame[f & 1], e->st));
+      return VX_OK;
+    };
+    if (max_frames > 0 && (rc = enqueue_frame(0))) return rc;
+    for (int f = 0; f < max_frames; f++) {
+      const bool ahead = f + 1 < max_frames;
+      if (ahead) {
+        if ((rc = enqueue_frame(f + 1))) return rc;
+        e->host_pos++;  // the backbone step of frame f + 1
+      }
+      HIPCHK(e, hipEventSynchronize(e->ev_frame[f & 1]));
+      const uint32_t *slot = e->h_frame + (f & 1) * (1 + NAC);
+      const uint32_t code = slot[0];
+      uint32_t codes[NAC];
+      memcpy(codes, slot + 1, sizeof codes);
+      if (code <= 1 && !opt.ignore_eos) {
+        if (ahead) {  // undo the speculative frame's step
+          HIPCHK(e, hipStreamSynchronize(e->st));
+          if ((rc = vx_set_position(e, e->host_pos - 1))) return rc;
+        }
+        break;
+      }
+      if (sem_out) sem_out[f] = code;
+      if (ac_out) memcpy(ac_out + (size_t)f * NAC, codes, sizeof codes);
+      frames++;
+      if (on_frame) on_frame(user, f, code, codes);
+    }
   }
   auto t2 = clk::now();
   if (on_stage) {

@@ -907,6 +907,138 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
   }
 }
 
+// ------------------------------------------------- top-p sampling (device)
+// sampleTopP (src/engine.ts:247-289) over the semantic logits, with the
+// generate() masking (index 0 and indices >= valid set to -inf,
+// src/engine.ts:2556-2563):
+//   s_i = f32(l_i / T); p_i = f32(exp(s_i - max)); q_i = f32(p_i / sum p)
+//   order by q descending, equal q by ascending index (a stable sort);
+//   cutoff = first rank whose running sum reaches top_p;
+//   r = u * (sum of the first cutoff q); pick the first rank whose running
+//   sum reaches r.
+// Sums are in f64 as in the reference (JS numbers), reduced in a fixed tree
+// order.  u = (z >> 11) * 2^-53 for z the next output of a splitmix64
+// stream whose state lives at *rng (advanced once per call).  One block of
+// TP_NT threads; keys sorted with a bitonic network in LDS.
+constexpr int TP_NT = 1024, TP_N = 16384;  // sort width (>= n, power of 2)
+__global__ __launch_bounds__(TP_NT) void topp_sample_kernel(const float *logits, int n, int valid,
+                                                            const double *params, uint64_t *rng,
+                                                            uint32_t *out) {
+  const double top_p = params[0], temp = params[1];  // in device memory: graphs stay valid
+  __shared__ uint64_t key[TP_N];
+  __shared__ double part[TP_NT];
+  __shared__ double red[TP_NT / 64];
+  __shared__ int pick[2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  auto scaled = [&](int i) -> float {
+    return (i > 0 && i < valid && i < n) ? (float)((double)logits[i] / temp) : -INFINITY;
+  };
+  // max
+  double mx = -INFINITY;
+  for (int i = tid; i < n; i += TP_NT) mx = fmax(mx, (double)scaled(i));
+  for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int w = 1; w < TP_NT / 64; w++) mx = fmax(mx, red[w]);
+  __syncthreads();
+  // sum of p in f64, fixed order: per thread, then tree
+  double s = 0.0;
+  for (int i = tid; i < n; i += TP_NT) s += (double)(float)exp((double)scaled(i) - mx);
+  part[tid] = s;
+  __syncthreads();
+  for (int o = TP_NT / 2; o > 0; o >>= 1) {
+    if (tid < o) part[tid] += part[tid + o];
+    __syncthreads();
+  }
+  const double sum = part[0];
+  __syncthreads();
+  // keys: q bits (q >= 0) high, inverted index low -> descending order is
+  // q descending, then index ascending
+  for (int i = tid; i < TP_N; i += TP_NT) {
+    uint64_t k = 0;
+    if (i < n) {
+      const float q = (float)((double)(float)exp((double)scaled(i) - mx) / sum);
+      k = ((uint64_t)__builtin_bit_cast(uint32_t, q) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+    }
+    key[i] = k;
+  }
+  __syncthreads();
+  for (int size = 2; size <= TP_N; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < TP_N / 2; i += TP_NT) {
+        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t a = key[lo], b = key[hi];
+        if ((a < b) == desc) {
+          key[lo] = b;
+          key[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  // running sums in sorted order: each thread a contiguous run of RUN
+  constexpr int RUN = TP_N / TP_NT;
+  auto qv = [&](int r) -> double { return (double)__builtin_bit_cast(float, (uint32_t)(key[r] >> 32)); };
+  double loc = 0.0;
+  for (int j = 0; j < RUN; j++) loc += qv(tid * RUN + j);
+  part[tid] = loc;
+  __syncthreads();
+  for (int o = 1; o < TP_NT; o <<= 1) {  // inclusive scan of the run totals
+    const double v = tid >= o ? part[tid - o] : 0.0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  const double base = tid ? part[tid - 1] : 0.0;
+  if (tid < 2) pick[tid] = TP_N;
+  __syncthreads();
+  {  // cutoff: first rank with running sum >= top_p
+    double c = base;
+    for (int j = 0; j < RUN; j++) {
+      c += qv(tid * RUN + j);
+      if (c >= top_p) {
+        atomicMin(&pick[0], tid * RUN + j + 1);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  const int cutoff = pick[0] < n ? pick[0] : n;
+  if (tid == 0) {
+    // resum = running sum at rank cutoff - 1, recomputed from its run
+    const int rr = cutoff - 1, t0 = rr / RUN;
+    double c = t0 ? part[t0 - 1] : 0.0;
+    for (int j = t0 * RUN; j <= rr; j++) c += qv(j);
+    uint64_t z = (*rng += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    part[0] = (double)(z >> 11) * 0x1p-53 * c;  // r (the scan is no longer needed at rank 0)
+  }
+  // part[0] is overwritten only after every thread read its base above
+  __syncthreads();
+  const double r = part[0];
+  __syncthreads();
+  {
+    double c = base;
+    for (int j = 0; j < RUN; j++) {
+      const int rank = tid * RUN + j;
+      if (rank >= cutoff) break;
+      c += qv(rank);
+      if (c >= r) {
+        atomicMin(&pick[1], rank);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int rank = pick[1] < cutoff ? pick[1] : 0;
+    *out = 0xFFFFFFFFu - (uint32_t)(key[rank] & 0xFFFFFFFFu);
+  }
+}
+
 // ------------------------------------------------------------- FM kernels
 // timeEmbedding (src/shaders.ts:579-602) for t
 __global__ void time_embed_kernel(float *out, float t) {

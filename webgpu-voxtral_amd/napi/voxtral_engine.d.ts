@@ -32,7 +32,8 @@ export interface TTSResult {
 }
 
 export interface GenerateOptions {
-  sampling?: 'top_p' | 'greedy';
+  /** 'top_p' (the reference's sampling, on the device), 'top_p_host' (the same on the host), 'greedy' */
+  sampling?: 'top_p' | 'top_p_host' | 'greedy';
   topP?: number;
   temperature?: number;
   seed?: number;

@@ -512,7 +512,9 @@ napi_value generate(napi_env env, napi_callback_info info) {
     napi_has_named_property(env, a.v[6], "sampling", &has);
     if (has) {
       napi_get_named_property(env, a.v[6], "sampling", &v);
-      j->opt.sampling = str(env, v) == "greedy" ? VX_SAMPLE_GREEDY : VX_SAMPLE_TOP_P;
+      const std::string m = str(env, v);
+      j->opt.sampling = m == "greedy" ? VX_SAMPLE_GREEDY
+                        : m == "top_p_host" ? VX_SAMPLE_TOP_P_HOST : VX_SAMPLE_TOP_P;
     }
     const char *keys[] = {"topP", "temperature", "seed", "ignoreEos"};
     for (int k = 0; k < 4; k++) {
@@ -529,8 +531,8 @@ napi_value generate(napi_env env, napi_callback_info info) {
       } else {
         d = num(env, v);
       }
-      if (k == 0) j->opt.top_p = (float)d;
-      if (k == 1) j->opt.temperature = (float)d;
+      if (k == 0) j->opt.top_p = d;
+      if (k == 1) j->opt.temperature = d;
       if (k == 2) j->opt.seed = (uint64_t)d;
       if (k == 3) j->opt.ignore_eos = d != 0;
     }

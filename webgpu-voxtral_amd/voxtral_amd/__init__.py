@@ -19,7 +19,7 @@ HEADER = os.path.join(os.path.dirname(PKG), "include", "voxtral_engine.h")
 
 VX_OK, VX_E_INVALID, VX_E_STATE, VX_E_DEVICE, VX_E_RANGE, VX_E_NOMEM = 0, -1, -2, -3, -4, -5
 EMBED_TOKEN, EMBED_AUDIO, EMBED_PRECOMPUTED, EMBED_CODES = 0, 1, 2, 3
-SAMPLE_TOP_P, SAMPLE_GREEDY = 0, 1
+SAMPLE_TOP_P, SAMPLE_GREEDY, SAMPLE_TOP_P_HOST = 0, 1, 2
 KERNEL_QKV, KERNEL_ATTN, KERNEL_OPROJ, KERNEL_GATEUP, KERNEL_DOWN = range(5)
 KERNEL_NAMES = ["qkv", "attn", "oproj", "gateup", "down"]
 
@@ -46,8 +46,8 @@ class Config(ctypes.Structure):
 
 
 class GenerateOptions(ctypes.Structure):
-    _fields_ = [("sampling", ctypes.c_int32), ("top_p", ctypes.c_float),
-                ("temperature", ctypes.c_float), ("seed", ctypes.c_uint64),
+    _fields_ = [("sampling", ctypes.c_int32), ("top_p", ctypes.c_double),
+                ("temperature", ctypes.c_double), ("seed", ctypes.c_uint64),
                 ("ignore_eos", ctypes.c_int32)]
 
 
@@ -73,6 +73,8 @@ _SIGS = {
     "vx_read_tensor": (_I32, [_VP, ctypes.c_char_p, _VP, ctypes.c_size_t]),
     "vx_is_ready": (_I32, [_VP]),
     "vx_prefill": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP]),
+    "vx_sample_top_p": (_I32, [_VP, _VP, _I32, _I32, ctypes.c_double, ctypes.c_double, _VP, _I32,
+                               _VP]),
     "vx_reset": (_I32, [_VP]),
     "vx_position": (_I32, [_VP]),
     "vx_set_position": (_I32, [_VP, _I32]),
@@ -338,7 +340,8 @@ class VoxtralEngine:
                 raise ValueError("voiceEmbeddings shorter than audioTokenCount rows")
         opt = GenerateOptions()
         self._lib.vx_generate_options_default(ctypes.byref(opt))
-        opt.sampling = SAMPLE_GREEDY if sampling == "greedy" else SAMPLE_TOP_P
+        opt.sampling = {"greedy": SAMPLE_GREEDY, "top_p": SAMPLE_TOP_P,
+                        "top_p_host": SAMPLE_TOP_P_HOST}[sampling]
         opt.top_p, opt.temperature, opt.seed, opt.ignore_eos = top_p, temperature, seed, int(ignore_eos)
         sem = np.zeros(max(1, max_frames), np.uint32)
         ac = np.zeros((max(1, max_frames), 36), np.uint32)
@@ -367,6 +370,17 @@ class VoxtralEngine:
                       "codecMs": stats.codec_ms, "totalMs": stats.total_ms,
                       "framesGenerated": n},
         }
+
+    def sample_top_p(self, logits, valid, top_p, temperature, state, on_device=True):
+        """sampleTopP (src/engine.ts:247-289) on caller logits with indices 0
+        and >= valid masked; returns (code, next splitmix64 state)."""
+        lg = _f32(logits)
+        st = ctypes.c_uint64(state)
+        code = ctypes.c_uint32()
+        self._check(self._lib.vx_sample_top_p(self._h, lg.ctypes.data, lg.size, int(valid),
+                                               float(top_p), float(temperature), ctypes.byref(st),
+                                               int(bool(on_device)), ctypes.byref(code)))
+        return code.value, st.value
 
     # -- measurement (no reference counterpart) --
     def time_backbone_steps(self, n, hold_position=False):
