@@ -223,6 +223,22 @@ def main():
             f"{prompt['mfma_frac_of_peak']:.1%} of MFMA peak); 500 decode steps "
             f"{prompt['decode_frames_per_s']:.1f} frames/s")
 
+    # ---- generate() end to end (prompt, kick, 200 frames, callbacks), per sampling mode
+    gen = None
+    if not args.no_long:
+        gen = {}
+        toks = list(np.random.default_rng(3).integers(0, 131072, 64))
+        for mode in ("top_p", "top_p_host", "greedy"):
+            eng.generate(toks, 0, 0, None, 8, sampling=mode, seed=1, ignore_eos=True)
+            t = time.perf_counter()
+            r = eng.generate(toks, 0, 0, None, 200, sampling=mode, seed=1, ignore_eos=True)
+            dt = time.perf_counter() - t
+            fr = r["stats"]["framesGenerated"]
+            gen[mode] = {"frames": fr, "s": round(dt, 4), "frames_per_s": round(fr / dt, 2),
+                         "x_realtime": round(fr / dt * 0.08, 2)}
+            log(f"[gpu] generate({mode}): {fr} frames in {dt * 1000:.0f} ms -> "
+                f"{fr / dt:.1f} frames/s = {fr / dt * 0.08:.1f}x real-time")
+
     # ---- long-context decode: 200 steps at positions 3896..4095 over a
     # synthetic N(0,1) KV cache (values f16-exact), context growing to 4096
     long_ctx = None
@@ -269,7 +285,8 @@ def main():
                      "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
         "roofline": roofline, "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()}
                                           for k, v in kern.items()},
-        "frame_loop": frame, "prompt": prompt, "long_context": long_ctx, "f16_kv_variant": f16kv,
+        "frame_loop": frame, "generate": gen, "prompt": prompt, "long_context": long_ctx,
+        "f16_kv_variant": f16kv,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
