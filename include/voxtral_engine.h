@@ -94,6 +94,21 @@ int vx_init_synthetic(vx_engine *e, uint64_t seed, float std);
  * plumbing for generator and loader checks). */
 int vx_read_tensor(vx_engine *e, const char *name, uint16_t *f16, size_t numel);
 
+/* loadWeightsFromHF, src/engine.ts:569-586 with src/weights.ts:478-669,
+ * from a local file instead of HTTP range requests: every tensor of the
+ * safetensors file whose name the engine uses is converted to f16 with the
+ * reference's rules (BF16: convertBF16toF16, src/weights.ts:94-138; F32:
+ * float32ToFloat16, :222-232; F16 as is) and loaded.  Codec decoder tensors
+ * (audio_tokenizer.*) and other names are skipped and counted.  Errors:
+ * unreadable file or header, an unsupported dtype ("Unsupported dtype for
+ * <name>: <dtype>"), a size or shape that differs from the engine's. */
+int vx_load_safetensors(vx_engine *e, const char *path, int32_t *n_loaded,
+                        int32_t *n_skipped);
+
+/* The two conversions above, on the host (no device needed). */
+void vx_bf16_to_f16(const uint16_t *bf16, uint16_t *f16, size_t n);
+void vx_f32_to_f16_trunc(const float *f32, uint16_t *f16, size_t n);
+
 /* isReady getter, src/engine.ts:2054-2056.  1 when every weight is loaded. */
 int vx_is_ready(const vx_engine *e);
 

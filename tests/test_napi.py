@@ -37,7 +37,8 @@ e.init().then(() => console.log(JSON.stringify({{names, ready, msg, init: 'ok'}}
               (err) => console.log(JSON.stringify({{names, ready, msg, init: err.message}})));
 """)
     r = json.loads(out.strip().splitlines()[-1])
-    assert r["names"] == sorted(["create", "destroy", "loadTensor", "initSynthetic", "isReady",
+    assert r["names"] == sorted(["create", "destroy", "loadTensor", "loadSafetensors",
+                                 "initSynthetic", "isReady",
                                  "reset", "position", "backboneStep", "fmForward",
                                  "setSemanticCode", "read", "generate"])
     assert r["ready"] is False
@@ -88,3 +89,47 @@ const m = require({json.dumps(JS)});
     assert [f[0] for f in r["frames"]] == list(range(5)) and r["late"] == 0
     assert [f[1] for f in r["frames"]] == r["sem"] and [f[2] for f in r["frames"]] == r["ac"]
     assert r["stages"][0] == ["backbone", None] and r["audio"] == 0
+
+
+@pytest.mark.gpu
+def test_load_weights_from_a_directory_of_shards(tmp_path):
+    """loadWeights(dir): every *.safetensors shard in name order, counts
+    summed; the engine then holds the converted weights."""
+    import numpy as np
+    from test_gpu_loader import to_bf16_bits, write_safetensors
+    import voxtral_amd as V
+    rng = np.random.default_rng(11)
+    fn = (1 + rng.standard_normal(3072) * 0.1).astype(np.float32)
+    write_safetensors(tmp_path / "model-00001-of-00002.safetensors",
+                      {"layers.0.ffn_norm.weight": ("BF16", to_bf16_bits(fn)),
+                       "audio_tokenizer.x": ("F32", np.zeros(2, np.float32))})
+    write_safetensors(tmp_path / "model-00002-of-00002.safetensors",
+                      {"norm.weight": ("F32", fn)})
+    (tmp_path / "README").write_text("not a shard")
+    script = f"""
+const m = require({json.dumps(JS)});
+(async () => {{
+  const e = new m.VoxtralEngine({{config: {{backbone: {{n_layers: 1}}}}, maxSeqLen: 16}});
+  await e.init();
+  e.initSynthetic(0, 0.02);
+  const r = await e.loadWeights({json.dumps(str(tmp_path))});
+  let err = '';
+  try {{ await e.loadWeights({json.dumps(str(tmp_path / "README"))}); }} catch (x) {{ err = x.message; }}
+  const normed = await e.debugBackboneStepFull(24);
+  e.destroy();
+  console.log(JSON.stringify({{r, err, normed: Array.from(normed.slice(0, 8))}}));
+}})().catch((err) => {{ console.error(err); process.exit(3); }});
+"""
+    print("[napi] loadWeights over two shards", flush=True)
+    r = json.loads(run_node(script, timeout=300).strip().splitlines()[-1])
+    assert r["r"] == {"loaded": 2, "skipped": 1}
+    assert "not a safetensors file" in r["err"]
+    g = V.VoxtralEngine(V.default_config(n_layers=1), max_seq_len=16).init()
+    try:
+        g.init_synthetic(0, 0.02)
+        g.load_tensor("layers.0.ffn_norm.weight", V.bf16_to_f16(to_bf16_bits(fn)), [3072])
+        g.load_tensor("norm.weight", V.f32_to_f16_trunc(fn), [3072])
+        _, normed = g.backbone_step(24)
+    finally:
+        g.destroy()
+    assert np.array_equal(np.float32(r["normed"]), normed[:8])

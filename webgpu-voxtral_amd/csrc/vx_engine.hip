@@ -19,6 +19,10 @@
 #include "../../include/voxtral_engine.h"
 #include "vx_kernels.h"
 #include "vx_prefill.h"
+#include "vx_loader.h"
+
+#include <fcntl.h>
+#include <unistd.h>
 
 using namespace vx;
 
@@ -799,6 +803,103 @@ int vx_load_tensor(vx_engine *e, const char *name, const uint16_t *f16, size_t n
   s.loaded = true;
   if (s.ptr == e->fm_time) e->tproj_ready = false;
   e->fm_packed_ready = false;
+  return VX_OK;
+}
+
+// ------------------------------------------------------------ safetensors
+void vx_bf16_to_f16(const uint16_t *in, uint16_t *out, size_t n) {
+  for (size_t i = 0; in && out && i < n; i++) out[i] = bf16_to_f16_ref(in[i]);
+}
+void vx_f32_to_f16_trunc(const float *in, uint16_t *out, size_t n) {
+  for (size_t i = 0; in && out && i < n; i++) {
+    uint32_t b;
+    memcpy(&b, in + i, 4);
+    out[i] = f32_to_f16_ref(b);
+  }
+}
+
+int vx_load_safetensors(vx_engine *e, const char *path, int32_t *n_loaded, int32_t *n_skipped) {
+  if (!e || !path) return VX_E_INVALID;
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0) return fail(e, VX_E_INVALID, "cannot open %s", path);
+  struct FdGuard {
+    int fd;
+    ~FdGuard() { close(fd); }
+  } guard{fd};
+  const off_t fsize = lseek(fd, 0, SEEK_END);
+  uint64_t hlen = 0;
+  if (fsize < 8 || pread(fd, &hlen, 8, 0) != 8 || hlen == 0 || hlen > (uint64_t)fsize - 8 ||
+      hlen > (64ull << 20))
+    return fail(e, VX_E_INVALID, "%s: not a safetensors file", path);
+  std::string hdr(hlen, '\0');
+  if (pread(fd, &hdr[0], hlen, 8) != (ssize_t)hlen)
+    return fail(e, VX_E_INVALID, "%s: short read of the header", path);
+  std::map<std::string, StEntry> entries;
+  std::string perr;
+  if (!StHeaderParser(hdr.data(), hdr.size()).parse(entries, perr))
+    return fail(e, VX_E_INVALID, "%s: bad safetensors header: %s", path, perr.c_str());
+  const uint64_t data0 = 8 + hlen;
+  // validate every tensor the engine takes before touching the device
+  std::vector<std::pair<const std::string *, Slot *>> work;
+  int skipped = 0;
+  for (auto &kv : entries) {
+    const char *comp = st_component(kv.first);
+    auto it = e->slots.find(kv.first);
+    if (!strcmp(comp, "other") || !strcmp(comp, "codec") || it == e->slots.end()) {
+      skipped++;  // codec decoder weights and names the engine does not use
+      continue;
+    }
+    const StEntry &t = kv.second;
+    const std::string &dt = t.dtype;
+    if (dt != "BF16" && dt != "F16" && dt != "F32")  // src/weights.ts:590-592
+      return fail(e, VX_E_INVALID, "Unsupported dtype for %s: %s", kv.first.c_str(), dt.c_str());
+    const uint64_t es = dt == "F32" ? 4 : 2;
+    Slot &sl = it->second;
+    if ((t.end - t.begin) != sl.numel * es || data0 + t.end > (uint64_t)fsize)
+      return fail(e, VX_E_INVALID, "%s: %llu bytes, expected %zu", kv.first.c_str(),
+                  (unsigned long long)(t.end - t.begin), sl.numel * es);
+    if (t.shape != sl.shape) return fail(e, VX_E_INVALID, "%s: shape mismatch", kv.first.c_str());
+    work.push_back({&kv.first, &sl});
+  }
+  // stream each tensor through a device staging buffer; convert on the GPU
+  constexpr size_t CH = 256u << 20;
+  void *stage = nullptr;
+  std::vector<char> host(CH);
+  HIPCHK(e, hipMalloc(&stage, CH));
+  struct DevGuard {
+    void *p;
+    ~DevGuard() { (void)hipFree(p); }
+  } dguard{stage};
+  for (auto &w : work) {
+    const StEntry &t = entries[*w.first];
+    const bool f32 = t.dtype == "F32", bf16 = t.dtype == "BF16";
+    const size_t es = f32 ? 4 : 2;
+    for (size_t done = 0; done < t.end - t.begin;) {
+      const size_t len = std::min(CH, (size_t)(t.end - t.begin) - done);
+      if (pread(fd, host.data(), len, (off_t)(data0 + t.begin + done)) != (ssize_t)len)
+        return fail(e, VX_E_INVALID, "%s: short read of %s", path, w.first->c_str());
+      uint16_t *dst = w.second->ptr + done / es;
+      if (!f32 && !bf16) {
+        HIPCHK(e, hipMemcpy(dst, host.data(), len, hipMemcpyHostToDevice));
+      } else {
+        HIPCHK(e, hipMemcpy(stage, host.data(), len, hipMemcpyHostToDevice));
+        if (bf16)
+          hipLaunchKernelGGL(bf16_to_f16_kernel, dim3(2048), dim3(256), 0, e->st, (const uint16_t *)stage,
+                             dst, len / 2);
+        else
+          hipLaunchKernelGGL(f32_to_f16_ref_kernel, dim3(2048), dim3(256), 0, e->st,
+                             (const uint32_t *)stage, dst, len / 4);
+        LAUNCHCHK(e);
+        HIPCHK(e, hipStreamSynchronize(e->st));
+      }
+      done += len;
+    }
+    w.second->loaded = true;
+  }
+  e->tproj_ready = false;
+  e->fm_packed_ready = false;
+  if (n_loaded) *n_loaded = (int32_t)work.size();
+  if (n_skipped) *n_skipped = skipped;
   return VX_OK;
 }
 

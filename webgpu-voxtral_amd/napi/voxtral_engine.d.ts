@@ -43,8 +43,10 @@ export interface GenerateOptions {
 export declare class VoxtralEngine {
   constructor(options?: EngineOptions);
   init(): Promise<void>;
-  loadWeights(baseUrl?: string): Promise<void>;
-  loadWeightsFromHF(url?: string): Promise<void>;
+  /** a local .safetensors file or a directory of shards in place of the base URL */
+  loadWeights(location: string): Promise<{ loaded: number; skipped: number }>;
+  loadWeightsFromHF(location: string): Promise<{ loaded: number; skipped: number }>;
+  loadSafetensors(file: string): { loaded: number; skipped: number };
   loadTensor(name: string, f16: Uint16Array, shape: number[]): void;
   initSynthetic(seed?: number, std?: number): void;
   readonly isReady: boolean;

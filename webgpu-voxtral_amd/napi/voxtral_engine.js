@@ -4,6 +4,7 @@
 // implemented on the Node-API addon voxtral_napi.node, which calls the C ABI
 // of libvoxtral_amd.so (include/voxtral_engine.h).  Plain ES2019 so that it
 // runs on the Node 12 of this image; voxtral_engine.d.ts carries the types.
+const fs = require('fs');
 const path = require('path');
 
 const ADDON = process.env.VOXTRAL_NAPI || path.join(__dirname, '..', 'lib', 'voxtral_napi.node');
@@ -56,14 +57,37 @@ class VoxtralEngine {
     return this._h;
   }
 
-  /** loadWeights(baseUrl) fetches over HTTP (src/engine.ts:539-566); this
-   *  build has no network path: pass tensors with loadTensor(). */
-  async loadWeights() {
-    throw new Error('loadWeights: no network loader in this build; use loadTensor(name, f16, shape)');
+  /** loadWeights (src/engine.ts:539-566) with a local path in place of the
+   *  base URL: one .safetensors file, or a directory whose *.safetensors
+   *  shards are loaded in name order.  Tensors convert as the reference's
+   *  loader converts them (BF16 -> f16 by convertBF16toF16, F32 -> f16 by
+   *  truncation, F16 as is); codec-decoder tensors are skipped.
+   *  Resolves to {loaded, skipped} summed over the shards. */
+  async loadWeights(location) {
+    if (typeof location !== 'string' || location.length === 0)
+      throw new Error('loadWeights: pass a local .safetensors file or a directory of shards');
+    const h = this._handle();
+    let files = [location];
+    if (fs.statSync(location).isDirectory())
+      files = fs.readdirSync(location).filter((f) => f.endsWith('.safetensors')).sort()
+        .map((f) => path.join(location, f));
+    if (files.length === 0) throw new Error(`loadWeights: no .safetensors files in ${location}`);
+    const total = { loaded: 0, skipped: 0 };
+    for (const f of files) {
+      const r = native.loadSafetensors(h, f);
+      total.loaded += r.loaded;
+      total.skipped += r.skipped;
+    }
+    return total;
   }
 
-  async loadWeightsFromHF() {
-    return this.loadWeights();
+  /** the same, for a single file */
+  loadSafetensors(file) {
+    return native.loadSafetensors(this._handle(), file);
+  }
+
+  async loadWeightsFromHF(location) {
+    return this.loadWeights(location);
   }
 
   /** one tensor of organizeWeights (src/engine.ts:659-743): f16 bits */

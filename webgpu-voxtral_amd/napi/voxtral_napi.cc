@@ -185,6 +185,25 @@ napi_value load_tensor(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+// loadSafetensors(h, path) -> {loaded, skipped}
+napi_value load_safetensors(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a) || a.n < 2) return nullptr;
+  vx_engine *e = handle(env, a.v[0]);
+  if (!e) return nullptr;
+  std::string path = str(env, a.v[1]);
+  int32_t loaded = 0, skipped = 0;
+  int rc = vx_load_safetensors(e, path.c_str(), &loaded, &skipped);
+  if (rc) return throw_vx(env, e, rc);
+  napi_value o, x;
+  NAPI_OK(env, napi_create_object(env, &o));
+  NAPI_OK(env, napi_create_int32(env, loaded, &x));
+  NAPI_OK(env, napi_set_named_property(env, o, "loaded", x));
+  NAPI_OK(env, napi_create_int32(env, skipped, &x));
+  NAPI_OK(env, napi_set_named_property(env, o, "skipped", x));
+  return o;
+}
+
 napi_value init_synthetic(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a) || a.n < 3) return nullptr;
@@ -560,6 +579,7 @@ napi_value init(napi_env env, napi_value exports) {
   } fns[] = {{"create", create},
              {"destroy", destroy},
              {"loadTensor", load_tensor},
+             {"loadSafetensors", load_safetensors},
              {"initSynthetic", init_synthetic},
              {"isReady", is_ready},
              {"reset", reset},

@@ -73,6 +73,9 @@ _SIGS = {
     "vx_read_tensor": (_I32, [_VP, ctypes.c_char_p, _VP, ctypes.c_size_t]),
     "vx_is_ready": (_I32, [_VP]),
     "vx_prefill": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP]),
+    "vx_load_safetensors": (_I32, [_VP, ctypes.c_char_p, _VP, _VP]),
+    "vx_bf16_to_f16": (None, [_VP, _VP, ctypes.c_size_t]),
+    "vx_f32_to_f16_trunc": (None, [_VP, _VP, ctypes.c_size_t]),
     "vx_sample_top_p": (_I32, [_VP, _VP, _I32, _I32, ctypes.c_double, ctypes.c_double, _VP, _I32,
                                _VP]),
     "vx_reset": (_I32, [_VP]),
@@ -121,6 +124,22 @@ def load_library(path=None):
 
 def exported_symbols():
     return list(_SIGS)
+
+
+def bf16_to_f16(bits):
+    """convertBF16toF16 (src/weights.ts:94-138) on uint16 BF16 bits."""
+    a = np.ascontiguousarray(bits, np.uint16)
+    out = np.empty_like(a)
+    load_library().vx_bf16_to_f16(a.ctypes.data, out.ctypes.data, a.size)
+    return out
+
+
+def f32_to_f16_trunc(values):
+    """float32ToFloat16 (src/weights.ts:222-232): truncating, no subnormals."""
+    a = np.ascontiguousarray(values, np.float32)
+    out = np.empty(a.shape, np.uint16)
+    load_library().vx_f32_to_f16_trunc(a.ctypes.data, out.ctypes.data, a.size)
+    return out
 
 
 def default_config(**over):
@@ -202,6 +221,14 @@ class VoxtralEngine:
         out = np.empty(int(numel), np.uint16)
         self._check(self._lib.vx_read_tensor(self._h, name.encode(), out.ctypes.data, out.size))
         return out
+
+    def load_safetensors(self, path):
+        """loadWeightsFromHF from a local safetensors file; returns
+        (tensors loaded, tensors skipped)."""
+        n, k = ctypes.c_int32(), ctypes.c_int32()
+        self._check(self._lib.vx_load_safetensors(self._h, os.fsencode(path), ctypes.byref(n),
+                                                  ctypes.byref(k)))
+        return n.value, k.value
 
     def init_synthetic(self, seed=0, std=0.02):
         self._check(self._lib.vx_init_synthetic(self._h, seed, std))
