@@ -95,6 +95,27 @@ def lib():
             "vxo_backbone_step_codes": (None, [c_vp]),
             "vxo_fm_forward": (None, [c_vp, F32]),
             "vxo_fm_forward_batched": (None, [c_vp, F32]),
+            # codec decoder (vx_oracle_codec.c)
+            "vxo_normalize_codebook": (None, [U16, U16, U16, c_int, c_int, c_float]),
+            "vxo_vq_lookup": (None, [U32, U16, F32, c_int, c_int, c_int]),
+            "vxo_fsq_dequant": (None, [U32, F32, c_int, c_int, c_int]),
+            "vxo_causal_conv1d": (None, [F32, U16, U16, F32, c_int, c_int, c_int, c_int, c_int]),
+            "vxo_conv_transpose_scale": (None, [U16, U16, F32, c_int, c_int, c_int]),
+            "vxo_conv_transpose1d": (None, [F32, U16, F32, F32, c_int, c_int, c_int, c_int, c_int]),
+            "vxo_batched_rmsnorm": (None, [F32, U16, F32, c_int, c_int, c_float]),
+            "vxo_batched_matvec_f16": (None, [U16, F32, F32, c_int, c_int, c_int]),
+            "vxo_qk_norm": (None, [F32, U16, c_int, c_int, c_int, c_float]),
+            "vxo_codec_attention": (None, [F32, F32, F32, F32, c_int, c_int, c_int, c_int]),
+            "vxo_codec_create": (c_vp, []),
+            "vxo_codec_destroy": (None, [c_vp]),
+            "vxo_codec_n_weights": (c_int, [c_vp]),
+            "vxo_codec_weight_name": (ctypes.c_char_p, [c_vp, c_int]),
+            "vxo_codec_weight_numel": (c_size, [c_vp, ctypes.c_char_p]),
+            "vxo_codec_weight": (c_vp, [c_vp, ctypes.c_char_p]),
+            "vxo_codec_set_weight": (c_int, [c_vp, ctypes.c_char_p, U16]),
+            "vxo_codec_init_synthetic": (c_int, [c_vp, c_u64, c_float]),
+            "vxo_codec_stop_count": (c_size, [c_int, c_int]),
+            "vxo_codec_decode": (c_int, [c_vp, U32, U32, c_int, c_int, F32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -330,3 +351,70 @@ class OracleEngine:
     def fm_forward(self, noise, batched=False):
         noise = np.ascontiguousarray(noise, np.float32)
         (lib().vxo_fm_forward_batched if batched else lib().vxo_fm_forward)(self._h, noise)
+
+
+# ---------------------------------------------------------- codec decoder
+CODEC_STOPS = ["concat", "after_input_conv",
+               "after_stage0_transformer", "after_stage0_conv_up",
+               "after_stage1_transformer", "after_stage1_conv_up",
+               "after_stage2_transformer", "after_stage2_conv_up",
+               "after_stage3_transformer", "audio"]
+
+
+class OracleCodec:
+    """CPU restatement of codecDecode (src/engine.ts:1402-1713) with the
+    codec weights by name (src/engine.ts:700-770)."""
+
+    def __init__(self):
+        self._h = lib().vxo_codec_create()
+        self._keep = {}
+
+    def close(self):
+        if self._h:
+            lib().vxo_codec_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def names(self):
+        L = lib()
+        return [L.vxo_codec_weight_name(self._h, i).decode()
+                for i in range(L.vxo_codec_n_weights(self._h))]
+
+    def init_synthetic(self, seed=0, std=0.02):
+        if lib().vxo_codec_init_synthetic(self._h, seed, std) != 0:
+            raise MemoryError("oracle codec weights")
+
+    def set_weight(self, name, bits):
+        bits = np.ascontiguousarray(bits, np.uint16).ravel()
+        if bits.size != lib().vxo_codec_weight_numel(self._h, name.encode()):
+            raise ValueError(f"bad size for {name}")
+        self._keep[name] = bits
+        if lib().vxo_codec_set_weight(self._h, name.encode(), bits) != 0:
+            raise KeyError(name)
+
+    def weight(self, name):
+        n = lib().vxo_codec_weight_numel(self._h, name.encode())
+        p = lib().vxo_codec_weight(self._h, name.encode())
+        if not n or not p:
+            raise KeyError(name)
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint16)), (n,))
+
+    def decode(self, semantic, acoustic, stop="audio"):
+        """codecDecode up to a debugCodecDecode intermediate (default the
+        waveform); semantic [T], acoustic [T][36]."""
+        sem = np.ascontiguousarray(semantic, np.uint32).ravel()
+        ac = np.ascontiguousarray(acoustic, np.uint32).ravel()
+        T = sem.size
+        if ac.size != 36 * T:
+            raise ValueError("acoustic codes must be [T][36]")
+        k = CODEC_STOPS.index(stop)
+        out = np.empty(lib().vxo_codec_stop_count(T, k), np.float32)
+        rc = lib().vxo_codec_decode(self._h, sem, ac, T, k, out)
+        if rc != 0:
+            raise RuntimeError(f"vxo_codec_decode failed ({rc})")
+        return out

@@ -38,6 +38,7 @@
  * golden vectors.  This file uses correctly rounded libm-style calls.
  */
 #include "vx_oracle.h"
+#include "vx_oracle_internal.h"
 
 #include <math.h>
 #include <stdio.h>
@@ -240,6 +241,17 @@ static void matvec_f16_multi(const uint16_t *A, const float *const *xs,
     matvec_row(A + (size_t)m * K, xs, nb, K, out);
     for (int b = 0; b < nb; b++) ys[b][m] = out[b];
   }
+}
+
+/* shared with vx_oracle_codec.c (vx_oracle_internal.h) */
+const float *vxo_i_h2f_table(void) {
+  h2f_init();
+  return g_h2f;
+}
+float vxo_i_tree_sum(float *sd) { return tree_sum(sd); }
+void vxo_i_matvec_multi(const uint16_t *A, const float *const *xs, float *const *ys, int nb,
+                        int M, int K) {
+  matvec_f16_multi(A, xs, ys, nb, M, K);
 }
 
 /* rmsNorm / rmsNormOffset, src/shaders.ts:137-183, 1278-1324 */

@@ -136,6 +136,44 @@ void vxo_fm_forward(vxo_engine *e, const float *noise);
  * output element as vxo_fm_forward. */
 void vxo_fm_forward_batched(vxo_engine *e, const float *noise);
 
+/* ------------------------------------------------------- codec decoder */
+/* vx_oracle_codec.c: codecDecode (src/engine.ts:1402-1713) and its shaders
+ * (src/shaders.ts:817-1110, 1432-1868). */
+void vxo_normalize_codebook(const uint16_t *sum, const uint16_t *usage, uint16_t *out,
+                            int n_entries, int dim, float eps);
+void vxo_vq_lookup(const uint32_t *codes, const uint16_t *cb, float *out, int T, int dim,
+                   int n_entries);
+void vxo_fsq_dequant(const uint32_t *codes, float *out, int n, int levels, int offset);
+void vxo_causal_conv1d(const float *in, const uint16_t *w, const uint16_t *g, float *out,
+                       int c_in, int c_out, int kernel, int n_frames, int stride);
+void vxo_conv_transpose_scale(const uint16_t *w, const uint16_t *g, float *scale, int c_in,
+                              int c_out, int kernel);
+void vxo_conv_transpose1d(const float *in, const uint16_t *w, const float *scale, float *out,
+                          int c_in, int c_out, int kernel, int n_out, int stride);
+void vxo_batched_rmsnorm(const float *in, const uint16_t *w, float *out, int dim, int T,
+                         float eps);
+void vxo_batched_matvec_f16(const uint16_t *A, const float *in, float *out, int M, int K,
+                            int T);
+void vxo_qk_norm(float *data, const uint16_t *w, int n_heads, int head_dim, int T, float eps);
+void vxo_codec_attention(const float *q, const float *k, const float *v, float *out,
+                         int n_heads, int head_dim, int T, int W);
+
+typedef struct vxo_codec vxo_codec;
+vxo_codec *vxo_codec_create(void);
+void vxo_codec_destroy(vxo_codec *c);
+int vxo_codec_n_weights(const vxo_codec *c);
+const char *vxo_codec_weight_name(const vxo_codec *c, int i);
+size_t vxo_codec_weight_numel(const vxo_codec *c, const char *name);
+const uint16_t *vxo_codec_weight(const vxo_codec *c, const char *name);
+int vxo_codec_set_weight(vxo_codec *c, const char *name, const uint16_t *data); /* borrowed */
+int vxo_codec_init_synthetic(vxo_codec *c, uint64_t seed, float std);
+/* stop: 0 concat input [T][292], 1 after_input_conv [T][1024],
+ * 2+2s after_stage{s}_transformer, 3+2s after_stage{s}_conv_up (s < 3),
+ * 9 audio [8T][240] (the names of debugCodecDecode, src/engine.ts:1719-1985) */
+size_t vxo_codec_stop_count(int T, int stop);
+int vxo_codec_decode(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int T, int stop,
+                     float *out);
+
 #ifdef __cplusplus
 }
 #endif

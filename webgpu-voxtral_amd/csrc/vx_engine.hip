@@ -1218,7 +1218,7 @@ static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int
     hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
                        W.attn_norm, e->cfg.norm_eps, e->pf_b);
     hipLaunchKernelGGL(pf_gemm_kernel<DIM>, dim3(QKV_ROWS / PF_BM, PF_NC / PF_BN, PF_S_QKV), blk, 0,
-                       st, W.wqkv, e->pf_b, e->pf_c, QKV_ROWS);
+                       st, W.wqkv, e->pf_b, e->pf_c, QKV_ROWS, PF_NC);
     hipLaunchKernelGGL(pf_qkv_epi_kernel, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c,
                        PF_S_QKV, e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0,
                        e->inv_freq);
@@ -1231,19 +1231,19 @@ static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int
     hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_attn, QD, n,
                        nullptr, 0.f, e->pf_b);
     hipLaunchKernelGGL(pf_gemm_kernel<QD>, dim3(DIM / PF_BM, PF_NC / PF_BN, PF_S_O), blk, 0, st,
-                       W.wo, e->pf_b, e->pf_c, DIM);
+                       W.wo, e->pf_b, e->pf_c, DIM, PF_NC);
     hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, PF_S_O,
                        e->pf_x);
     hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
                        W.ffn_norm, e->cfg.norm_eps, e->pf_b);
     // W1 and W3 are adjacent in the arena: one GEMM over the stacked rows
     hipLaunchKernelGGL(pf_gemm_kernel<DIM>, dim3(2 * HID / PF_BM, PF_NC / PF_BN), blk, 0, st, W.w1,
-                       e->pf_b, e->pf_c, 2 * HID);
+                       e->pf_b, e->pf_c, 2 * HID, PF_NC);
     hipLaunchKernelGGL(pf_swiglu_epi_kernel, dim3(n, HID / 256), blk, 0, st, e->pf_c, e->pf_act);
     hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_act, HID, n,
                        nullptr, 0.f, e->pf_b);
     hipLaunchKernelGGL(pf_gemm_kernel<HID>, dim3(DIM / PF_BM, PF_NC / PF_BN, PF_S_DOWN), blk, 0, st,
-                       W.w2, e->pf_b, e->pf_c, DIM);
+                       W.w2, e->pf_b, e->pf_c, DIM, PF_NC);
     hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM,
                        PF_S_DOWN, e->pf_x);
   }

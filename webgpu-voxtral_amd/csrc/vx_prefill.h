@@ -26,14 +26,15 @@ static_assert(PF_NC % PF_BN == 0, "column tiles");
 // 16 x 16); k in chunks of 32 staged through LDS as [k group][row|col][8],
 // double-buffered, with the global loads two chunks ahead.  The k range is
 // split S ways over blockIdx.z (S = gridDim.z) so that narrow matrices fill
-// the chip; slab s of C holds the partial sum of split s.
-// Grid: (M / PF_BM, PF_NC / PF_BN, S).  C: [S][PF_NC][ldc] f32.
+// the chip; slab s of C holds the partial sum of split s.  B has nc columns
+// (a multiple of PF_BN; the prefill uses PF_NC).
+// Grid: (M / PF_BM, nc / PF_BN, S).  C: [S][nc][ldc] f32.
 template <int K>
 __global__ __launch_bounds__(256) void pf_gemm_kernel(const uint16_t *W, const h8 *B, float *C,
-                                                      int ldc) {
+                                                      int ldc, int nc) {
   static_assert(K % 32 == 0, "k chunks");
   const int S = gridDim.z, NCH = K / 32 / S, ch0 = blockIdx.z * NCH;
-  C += (size_t)blockIdx.z * PF_NC * ldc;
+  C += (size_t)blockIdx.z * nc * ldc;
   __shared__ __attribute__((aligned(16))) h8 As[2][4][PF_BM];
   __shared__ __attribute__((aligned(16))) h8 Bs[2][4][PF_BN];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -53,7 +54,7 @@ __global__ __launch_bounds__(256) void pf_gemm_kernel(const uint16_t *W, const h
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int p = tid + 256 * i, kg = p >> 8, col = p & 255;
-      rb[r][i] = *(const u32x4 *)(B + (size_t)((ch0 + ch) * 4 + kg) * PF_NC + n0 + col);
+      rb[r][i] = *(const u32x4 *)(B + (size_t)((ch0 + ch) * 4 + kg) * nc + n0 + col);
     }
   };
   auto lstore = [&](int buf, int r) {
