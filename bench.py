@@ -10,8 +10,10 @@ all inputs resident in HBM.  value = decode steps (frames) per second.
 
 Also reported: the full frame loop (backbone step + 3-layer flow-matching
 CFG Euler loop, greedy semantic code on the device, 500 frames from
-context 512) as x-real-time (one frame = 80 ms of audio), the roofline of
-the dominant kernel, and the CPU oracle timed on the host cores.
+context 512) as x-real-time (one frame = 80 ms of audio), generate() end to
+end (prompt, frames, codec decode) per sampling mode, the codec decoder on
+its own, the roofline of the dominant kernel, and the CPU oracle timed on
+the host cores.
 Diagnostics go to stderr.
 """
 import argparse
@@ -38,6 +40,24 @@ EMB_CODES_BYTES = 37 * 3072 * 2           # 37-row multi-codebook sum
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def codec_flops(T):
+    """Algorithmic flops of the codec decoder for T frames (1 multiply-add =
+    2 flops): input conv 292*3 -> 1024; per stage 2 layers of q,k,v,o
+    (1024^2 each), gate/up (2 x 4096x1024), down (1024x4096) over the
+    stage's tokens plus the windowed attention; stride-2 transposed convs
+    (2 taps x 1024 channels per output); output conv 1024*7 -> 240."""
+    f = 2 * T * 1024 * 292 * 3
+    tt = T
+    for s, w in enumerate((2, 4, 8, 16)):
+        f += 2 * 2 * tt * (4 * 1024 * 1024 + 3 * 4096 * 1024)
+        f += 2 * 2 * tt * 8 * 128 * w * 2
+        if s < 3:
+            f += 2 * (2 * tt) * 1024 * 2048
+            tt *= 2
+    f += 2 * tt * 240 * 1024 * 7
+    return f
 
 
 def measured_traffic(kernel):
@@ -105,6 +125,30 @@ def measure_prompt(eng, reps=5):
                     "64 voice rows included), median of 4 after 1 warm-up"}
 
 
+def measure_codec(eng, T=250, reps=3):
+    """codecDecode of T frames of random codes, wall time per call."""
+    rng = np.random.default_rng(5)
+    sem = rng.integers(2, 8194, T).astype(np.uint32)
+    ac = rng.integers(2, 23, (T, 36)).astype(np.uint32)
+    eng.codec_decode(sem, ac)
+    t = time.perf_counter()
+    for _ in range(reps):
+        eng.codec_decode(sem, ac)
+    cms = (time.perf_counter() - t) / reps * 1000.0
+    fl = codec_flops(T)
+    codec = {"frames": T, "audio_s": T * 0.08, "ms": round(cms, 3),
+             "x_realtime": round(T * 0.08 / (cms * 1e-3), 1),
+             "algorithmic_GFLOP": round(fl / 1e9, 2),
+             "TFLOPs": round(fl / (cms * 1e-3) / 1e12, 2),
+             "mfma_issued_frac_of_peak": round(2 * fl / (cms * 1e-3) / 2.5e15, 4),
+             "note": "wall time per call incl. code upload and audio readback; "
+                     "f16 weights x hi/lo f16 activations on MFMA (2 issued flops per "
+                     "algorithmic flop)"}
+    log(f"[gpu] codec decode {T} frames: {cms:.2f} ms = {codec['x_realtime']:.0f}x real-time, "
+        f"{codec['TFLOPs']:.1f} TFLOP/s algorithmic")
+    return codec
+
+
 def cpu_baseline(target_s):
     """The oracle (C restatement of the reference kernels, OpenMP) on the
     host: full-depth 26-layer decode steps at context 512, no LM head."""
@@ -148,6 +192,9 @@ def main():
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="also run a plain device copy of this many MB (a known-traffic "
                          "kernel for scaling hardware byte counters)")
+    ap.add_argument("--section", choices=["all", "codec"], default="all",
+                    help="codec: only the codec decoder measurement (a 1-layer engine), "
+                         "printed as {\"codec\": ...}")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the frame loop runs on a single MI355X "
@@ -167,6 +214,12 @@ def main():
         log(f"[gpu] copy probe: 3 x {args.copy_probe_mb} MB device copy")
 
     import voxtral_amd as V
+    if args.section == "codec":
+        eng = V.VoxtralEngine(V.default_config(n_layers=1), max_seq_len=64).init()
+        eng.init_synthetic(0, 0.02)
+        print(json.dumps({"codec": measure_codec(eng)}), flush=True)
+        eng.destroy()
+        return
     t0 = time.time()
     eng = prefilled_engine(V, kv_f16=False)
     log(f"[gpu] weights + {CTX}-token prefill in {time.time() - t0:.1f}s")
@@ -235,9 +288,14 @@ def main():
             dt = time.perf_counter() - t
             fr = r["stats"]["framesGenerated"]
             gen[mode] = {"frames": fr, "s": round(dt, 4), "frames_per_s": round(fr / dt, 2),
-                         "x_realtime": round(fr / dt * 0.08, 2)}
+                         "x_realtime": round(fr / dt * 0.08, 2),
+                         "codec_ms": round(r["stats"]["codecMs"], 3),
+                         "audio_samples": int(r["audio"].size)}
             log(f"[gpu] generate({mode}): {fr} frames in {dt * 1000:.0f} ms -> "
                 f"{fr / dt:.1f} frames/s = {fr / dt * 0.08:.1f}x real-time")
+
+    # ---- codec decoder: 250 frames (20 s of audio) of random codes
+    codec = None if args.no_long else measure_codec(eng)
 
     # ---- long-context decode: 200 steps at positions 3896..4095 over a
     # synthetic N(0,1) KV cache (values f16-exact), context growing to 4096
@@ -285,7 +343,8 @@ def main():
                      "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
         "roofline": roofline, "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()}
                                           for k, v in kern.items()},
-        "frame_loop": frame, "generate": gen, "prompt": prompt, "long_context": long_ctx,
+        "frame_loop": frame, "generate": gen, "prompt": prompt, "codec": codec,
+        "long_context": long_ctx,
         "f16_kv_variant": f16kv,
         "cpu_baseline": cpu,
     }

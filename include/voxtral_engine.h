@@ -63,6 +63,10 @@ typedef struct vx_config {
    * more than 1e-2 after 26 random-weight layers, so parity with the
    * reference holds for 0 only. */
   int32_t kv_f16;
+  /* Codec decoder (no reference field; the reference always has one,
+   * src/engine.ts:1402-1713): 1 = its weights are part of the engine and
+   * generate() returns audio, the default; 0 = the frame loop only. */
+  int32_t codec;
 } vx_config;
 
 /* defaultConfig, src/types.ts:70-122 */
@@ -206,7 +210,7 @@ typedef struct vx_generate_options {
 typedef struct vx_generate_stats {
   double backbone_ms; /* prefill (TTSResult.stats.backboneMs) */
   double fm_ms;       /* frame loop (stats.fmMs) */
-  double codec_ms;    /* 0: the codec decoder is not part of this library */
+  double codec_ms;    /* codec decode of the generated codes (0 without audio_out) */
   double total_ms;
   int32_t frames_generated;
 } vx_generate_stats;
@@ -221,15 +225,40 @@ typedef void (*vx_stage_cb)(void *user, int32_t stage, double done_ms);
 void vx_generate_options_default(vx_generate_options *o);
 
 /* generate(tokens, audioTokenStart, audioTokenCount, voiceEmbeddings,
- * maxFrames, onFrame, onStage), src/engine.ts:2416-2616, without the codec
- * decode.  voice: f32[audio_count][dim] or NULL.  semantic_out[max_frames]
- * and acoustic_out[max_frames][36] receive the codes (nullable). */
+ * maxFrames, onFrame, onStage), src/engine.ts:2416-2616.  voice:
+ * f32[audio_count][dim] or NULL.  semantic_out[max_frames] and
+ * acoustic_out[max_frames][36] receive the codes; audio_out
+ * f32[max_frames * VX_FRAME_SAMPLES] receives codecDecode of the generated
+ * frames (TTSResult.audio; 1920 samples per frame).  All three are
+ * nullable; audio_out needs an engine created with cfg.codec = 1. */
 int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens,
                 int32_t audio_start, int32_t audio_count, const float *voice,
                 int32_t max_frames, const vx_generate_options *opt,
                 vx_frame_cb on_frame, vx_stage_cb on_stage, void *user,
-                uint32_t *semantic_out, uint32_t *acoustic_out,
+                uint32_t *semantic_out, uint32_t *acoustic_out, float *audio_out,
                 vx_generate_stats *stats);
+
+/* ------------------------------------------------------- codec decoder */
+#define VX_FRAME_SAMPLES 1920     /* 80 ms of 24 kHz audio per frame */
+#define VX_CODEC_MAX_FRAMES 65536 /* 87 minutes of audio per call */
+/* codecDecode(semanticCodes, acousticCodes), src/engine.ts:1402-1713:
+ * semantic[n_frames], acoustic[n_frames][36] (values as generate() emits
+ * them: semantic 2..8193 indexes the 8192-row VQ codebook directly, as the
+ * reference's vqLookup does, rows past it read as zero; acoustic 2..22) ->
+ * audio f32[n_frames * VX_FRAME_SAMPLES]. */
+int vx_codec_decode(vx_engine *e, const uint32_t *semantic, const uint32_t *acoustic,
+                    int32_t n_frames, float *audio);
+
+/* debugCodecDecode (src/engine.ts:1719-1985): the decoder up to one of its
+ * intermediates.  out must hold vx_codec_stop_count(n_frames, stop) floats. */
+#define VX_CODEC_STOP_CONCAT 0      /* [T][292] VQ embedding | FSQ values */
+#define VX_CODEC_STOP_INPUT_CONV 1  /* after_input_conv [T][1024] */
+#define VX_CODEC_STOP_STAGE0 2      /* after_stage{s}_transformer: 2 + 2s; */
+                                    /* after_stage{s}_conv_up: 3 + 2s (s < 3) */
+#define VX_CODEC_STOP_AUDIO 9       /* audio [8T][240] */
+int vx_codec_decode_debug(vx_engine *e, const uint32_t *semantic, const uint32_t *acoustic,
+                          int32_t n_frames, int32_t stop, float *out, size_t out_count);
+size_t vx_codec_stop_count(int32_t n_frames, int32_t stop);
 
 /* sampleTopP on caller logits (test plumbing): logits f32[n] with indices
  * 0 and >= valid masked, n <= 16384.  *state: the splitmix64 state of the

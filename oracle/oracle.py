@@ -116,6 +116,7 @@ def lib():
             "vxo_codec_init_synthetic": (c_int, [c_vp, c_u64, c_float]),
             "vxo_codec_stop_count": (c_size, [c_int, c_int]),
             "vxo_codec_decode": (c_int, [c_vp, U32, U32, c_int, c_int, F32]),
+            "vxo_codec_decode_all": (c_int, [c_vp, U32, U32, c_int, c_vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -418,3 +419,17 @@ class OracleCodec:
         if rc != 0:
             raise RuntimeError(f"vxo_codec_decode failed ({rc})")
         return out
+
+    def decode_all(self, semantic, acoustic):
+        """every debugCodecDecode intermediate by name, in one pass"""
+        sem = np.ascontiguousarray(semantic, np.uint32).ravel()
+        ac = np.ascontiguousarray(acoustic, np.uint32).ravel()
+        T = sem.size
+        if ac.size != 36 * T:
+            raise ValueError("acoustic codes must be [T][36]")
+        outs = [np.empty(lib().vxo_codec_stop_count(T, k), np.float32) for k in range(10)]
+        ptrs = (ctypes.c_void_p * 10)(*[o.ctypes.data for o in outs])
+        rc = lib().vxo_codec_decode_all(self._h, sem, ac, T, ctypes.cast(ptrs, ctypes.c_void_p))
+        if rc != 0:
+            raise RuntimeError(f"vxo_codec_decode_all failed ({rc})")
+        return dict(zip(CODEC_STOPS, outs))

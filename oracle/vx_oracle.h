@@ -173,6 +173,9 @@ int vxo_codec_init_synthetic(vxo_codec *c, uint64_t seed, float std);
 size_t vxo_codec_stop_count(int T, int stop);
 int vxo_codec_decode(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int T, int stop,
                      float *out);
+/* every intermediate k with outs[k] != NULL (outs[10]) in one pass */
+int vxo_codec_decode_all(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int T,
+                         float *const *outs);
 
 #ifdef __cplusplus
 }

@@ -20,7 +20,8 @@
  *   windowed ALiBi attention  a dense f64 attention with an explicit
  *                        causal-window mask and bias
  *   whole decoder        a float64 torch model of the decoder written from
- *                        the architecture (tests/oracle_np.py)
+ *                        the architecture (tests/codec_f64.py), every
+ *                        intermediate
  * Semantic codes >= 8192 index past the 8192-row codebook in the reference
  * (vqLookup has no bound check; WebGPU clamps such reads in an
  * implementation-defined way).  Here they read a zero row: parity unpinned
@@ -423,9 +424,14 @@ static float *fa(size_t n) {
   return p;
 }
 
-int vxo_codec_decode(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int T, int stop,
-                     float *out) {
-  if (T < 1 || stop < 0 || stop > 9) return -1;
+/* codecDecode with every debugCodecDecode intermediate whose outs[k] is set
+ * (outs[10], entries nullable); stops after the last one requested */
+int vxo_codec_decode_all(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int T,
+                         float *const *outs) {
+  int last = -1;
+  for (int k = 0; k < 10; k++)
+    if (outs[k]) last = k;
+  if (T < 1 || last < 0) return -1;
   for (int i = 0; i < c->n_slots; i++)
     if (!*c->slots[i].slot) return -2;
   g_h = vxo_i_h2f_table();
@@ -443,8 +449,8 @@ int vxo_codec_decode(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int 
   free(cb);
   free(sem_e);
   free(ac_f);
-  if (stop == 0) {
-    memcpy(out, cat, (size_t)T * CIN * 4);
+  if (outs[0]) memcpy(outs[0], cat, (size_t)T * CIN * 4);
+  if (last == 0) {
     free(cat);
     return 0;
   }
@@ -454,8 +460,13 @@ int vxo_codec_decode(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int 
         *up = fa((size_t)Tmax * CHID), *nxt = fa((size_t)Tmax * CD);
   vxo_causal_conv1d(cat, c->in_w, c->in_g, cur, CIN, CD, 3, T, 1);
   free(cat);
-  int curT = T, at = 1, rc = 0;
-  if (stop == at) goto done;
+  int curT = T, at = 1;
+#define EMIT()                                                          \
+  do {                                                                  \
+    if (outs[at]) memcpy(outs[at], cur, (size_t)curT * CD * 4);         \
+    if (at == last) goto cleanup;                                       \
+  } while (0)
+  EMIT();
   for (int s = 0; s < CSTAGES; s++) {
     for (int l = 0; l < CLPS; l++) {
       const cx_layer *L = &c->L[s][l];
@@ -482,7 +493,7 @@ int vxo_codec_decode(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int 
       for (size_t i = 0; i < n; i++) cur[i] = o[i] * H(L->ffn_scale[i % CD]) + res[i];
     }
     at = 2 + 2 * s;
-    if (stop == at) goto done;
+    EMIT();
     if (kStageStride[s] > 1) {
       float scale[CD];
       vxo_conv_transpose_scale(c->up_w[s], c->up_g[s], scale, CD, CD, kStageKernel[s]);
@@ -494,15 +505,21 @@ int vxo_codec_decode(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int 
       nxt = tmp;
       curT = newT;
       at = 3 + 2 * s;
-      if (stop == at) goto done;
+      EMIT();
     }
   }
-  vxo_causal_conv1d(cur, c->out_w, c->out_g, out, CD, CPATCH, 7, curT, 1);
-  goto cleanup;
-done:
-  memcpy(out, cur, (size_t)curT * CD * 4);
+#undef EMIT
+  vxo_causal_conv1d(cur, c->out_w, c->out_g, outs[9], CD, CPATCH, 7, curT, 1);
 cleanup:;
   float *bufs[] = {cur, res, xn, q, k, v, ao, o, gate, up, nxt};
   for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) free(bufs[i]);
-  return rc;
+  return 0;
+}
+
+int vxo_codec_decode(vxo_codec *c, const uint32_t *sem, const uint32_t *ac, int T, int stop,
+                     float *out) {
+  if (stop < 0 || stop > 9 || !out) return -1;
+  float *outs[10] = {0};
+  outs[stop] = out;
+  return vxo_codec_decode_all(c, sem, ac, T, outs);
 }

@@ -37,7 +37,7 @@ e.init().then(() => console.log(JSON.stringify({{names, ready, msg, init: 'ok'}}
               (err) => console.log(JSON.stringify({{names, ready, msg, init: err.message}})));
 """)
     r = json.loads(out.strip().splitlines()[-1])
-    assert r["names"] == sorted(["create", "destroy", "loadTensor", "loadSafetensors",
+    assert r["names"] == sorted(["create", "destroy", "loadTensor", "loadSafetensors", "codecDecode",
                                  "initSynthetic", "isReady",
                                  "reset", "position", "backboneStep", "fmForward",
                                  "setSemanticCode", "read", "generate"])
@@ -67,10 +67,14 @@ const m = require({json.dumps(JS)});
     (st, ms) => stages.push([st, ms === undefined ? null : 1]),
     {{sampling: 'greedy', seed: 3, ignoreEos: true}});
   settled = true;
+  const dec = await e.codecDecode(r.semanticCodes, [].concat(...r.acousticCodes));
+  const redecoded = dec.length === r.audio.length && dec.every((v, i) => v === r.audio[i]);
   const normed = await e.debugBackboneStepFull(24);
   e.destroy();
   console.log(JSON.stringify({{sem: r.semanticCodes, ac: r.acousticCodes, n: r.stats.framesGenerated,
-                               frames, stages, late, audio: r.audio.length, normed0: normed[0]}}));
+                               redecoded,
+                               frames, stages, late, audio: r.audio.length,
+                               audio_head: Array.from(r.audio.slice(0, 64)), normed0: normed[0]}}));
 }})().catch((err) => {{ console.error(err); process.exit(3); }});
 """
     print("[napi] node generate, 2 layers, 5 frames", flush=True)
@@ -88,7 +92,11 @@ const m = require({json.dumps(JS)});
     assert r["n"] == 5 and r["sem"] == py["semanticCodes"] and r["ac"] == py["acousticCodes"]
     assert [f[0] for f in r["frames"]] == list(range(5)) and r["late"] == 0
     assert [f[1] for f in r["frames"]] == r["sem"] and [f[2] for f in r["frames"]] == r["ac"]
-    assert r["stages"][0] == ["backbone", None] and r["audio"] == 0
+    assert r["stages"][0] == ["backbone", None] and r["stages"][-1][0] == "codec"
+    # TTSResult.audio: codecDecode of the 5 frames, as through Python
+    assert r["audio"] == 5 * 1920 == py["audio"].size
+    assert r["redecoded"]
+    assert np.array_equal(np.float32(r["audio_head"]), py["audio"][:64])
 
 
 @pytest.mark.gpu

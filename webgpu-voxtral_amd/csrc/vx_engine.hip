@@ -19,6 +19,7 @@
 #include "../../include/voxtral_engine.h"
 #include "vx_kernels.h"
 #include "vx_prefill.h"
+#include "vx_codec.h"
 #include "vx_loader.h"
 
 #include <fcntl.h>
@@ -39,8 +40,22 @@ struct Slot {
   uint16_t *ptr;
   std::vector<int64_t> shape;
   size_t numel;
-  bool is_norm;
+  bool is_norm;  // gains and scales: synthetic weights centred on 1
   bool loaded;
+};
+
+// codec decoder weights (src/engine.ts:700-770).  wq, wk, wv are adjacent
+// (wqkv), and so are w1, w3 (w13), so each pair is one stacked GEMM.
+struct CodecLayerW {
+  uint16_t *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *wqkv = nullptr,
+           *wo = nullptr, *attn_scale = nullptr, *ffn_norm = nullptr, *w13 = nullptr,
+           *w2 = nullptr, *ffn_scale = nullptr;
+};
+struct CodecW {
+  uint16_t *in_w = nullptr, *in_g = nullptr, *out_w = nullptr, *out_g = nullptr,
+           *cb_sum = nullptr, *cb_usage = nullptr;
+  uint16_t *up_w[CX_STAGES - 1] = {}, *up_g[CX_STAGES - 1] = {};
+  CodecLayerW L[CX_STAGES][CX_LPS];
 };
 
 // FNV-1a 64 of "fm.noise": generator stream of the per-frame FM noise
@@ -109,6 +124,28 @@ struct vx_engine {
   uint32_t *h_frame = nullptr;  // [2][1 + NAC]
   hipEvent_t ev_frame[2] = {nullptr, nullptr};
   hipGraphExec_t fm_topp_exec = nullptr, frame_topp_exec = nullptr;
+
+  // codec decoder: weights; derived operands (normalised codebook, conv
+  // weights in GEMM order, weight-norm scales), rebuilt after weight loads;
+  // per-decode buffers sized for cx_cap frames
+  bool codec_on = false, codec_ready = false;
+  CodecW cw;
+  void *cx_parena = nullptr;
+  uint16_t *cx_cb = nullptr, *cx_ain = nullptr, *cx_aout = nullptr, *cx_aup[CX_STAGES - 1] = {};
+  float *cx_rs_in = nullptr, *cx_rs_out = nullptr, *cx_s_up[CX_STAGES - 1] = {};
+  void *cx_arena = nullptr;
+  int cx_cap = 0;
+  float *cx_x = nullptr, *cx_x2 = nullptr, *cx_q = nullptr, *cx_k = nullptr, *cx_v = nullptr,
+        *cx_attn = nullptr, *cx_c = nullptr, *cx_audio = nullptr;
+  h8 *cx_b = nullptr;
+  uint32_t *cx_sem = nullptr, *cx_ac = nullptr;
+  int cx_chunk = CX_MAXT;  // tokens per codec GEMM chunk (multiple of 128)
+
+  void weights_changed() {
+    tproj_ready = false;
+    fm_packed_ready = false;
+    codec_ready = false;
+  }
 
   void *kc(int l) const { return (char *)kv + (size_t)(2 * l) * NKV * max_seq * HD * kv_elem; }
   void *vc(int l) const { return (char *)kv + (size_t)(2 * l + 1) * NKV * max_seq * HD * kv_elem; }
@@ -509,6 +546,7 @@ int vx_config_default(vx_config *c) {
   c->acoustic_levels = 21;
   c->audio_vocab = 9088;
   c->kv_f16 = 0;
+  c->codec = 1;
   return VX_OK;
 }
 
@@ -534,7 +572,8 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
                 "FFN 9216, 36 acoustic dims, semantic vocab 8320");
   if (cfg.n_layers < 1 || cfg.n_layers > 64 || cfg.fm_layers < 1 || cfg.fm_layers > 16 ||
       cfg.nfe < 2 || cfg.nfe > 64 || cfg.vocab_size < 25 || cfg.audio_vocab < 9022 ||
-      cfg.acoustic_levels < 2 || (cfg.kv_f16 != 0 && cfg.kv_f16 != 1))
+      cfg.acoustic_levels < 2 || (cfg.kv_f16 != 0 && cfg.kv_f16 != 1) ||
+      (cfg.codec != 0 && cfg.codec != 1))
     return fail(nullptr, VX_E_INVALID, "config out of range");
   if (max_seq < 1 || max_seq > (1 << 20))
     return fail(nullptr, VX_E_INVALID, "max_seq_len %d out of range", max_seq);
@@ -608,6 +647,34 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   place(&e->fm_norm, DIM);
   place(&e->fm_sem, (size_t)SEMV * DIM);
   place(&e->fm_ac, (size_t)NAC * DIM);
+  e->codec_on = cfg.codec != 0;
+  CodecW &cw = e->cw;
+  if (e->codec_on) {
+    place(&cw.in_w, (size_t)CD * CIN * CK_IN);
+    place(&cw.in_g, CD);
+    for (int st = 0; st < CX_STAGES; st++) {
+      for (auto &L : cw.L[st]) {
+        place(&L.wqkv, (size_t)3 * CD * CD);
+        place(&L.wo, (size_t)CD * CD);
+        place(&L.w13, (size_t)2 * CHID * CD);
+        place(&L.w2, (size_t)CD * CHID);
+        place(&L.attn_norm, CD);
+        place(&L.q_norm, CD);
+        place(&L.k_norm, CD);
+        place(&L.attn_scale, CD);
+        place(&L.ffn_norm, CD);
+        place(&L.ffn_scale, CD);
+      }
+      if (st < CX_STAGES - 1) {
+        place(&cw.up_w[st], (size_t)CD * CD * CK_UP);
+        place(&cw.up_g[st], CD);
+      }
+    }
+    place(&cw.out_w, (size_t)CPATCH * CD * CK_OUT);
+    place(&cw.out_g, CPATCH);
+    place(&cw.cb_sum, (size_t)CSEM * CSEMD);
+    place(&cw.cb_usage, CSEM);
+  }
   if (hipMalloc(&e->warena, total) != hipSuccess) {
     vx_destroy(e);
     return fail(nullptr, VX_E_NOMEM, "hipMalloc of %zu weight bytes failed", total);
@@ -638,6 +705,75 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   add_slot(e, "acoustic_transformer.norm.weight", e->fm_norm, {DIM}, true);
   add_slot(e, "acoustic_transformer.semantic_codebook_output.weight", e->fm_sem, {SEMV, DIM}, false);
   add_slot(e, "acoustic_transformer.acoustic_codebook_output.weight", e->fm_ac, {NAC, DIM}, false);
+  if (e->codec_on) {
+    // codec decoder tensors (src/engine.ts:700-770); weight-norm convs keep
+    // v (original1) and g (original0) as stored
+    const std::string P = "audio_tokenizer.";
+    const int64_t cd = CD, hid = CHID;
+    add_slot(e, P + "decoder_blocks.0.conv.parametrizations.weight.original1", cw.in_w,
+             {cd, CIN, CK_IN}, false);
+    add_slot(e, P + "decoder_blocks.0.conv.parametrizations.weight.original0", cw.in_g, {cd, 1, 1},
+             true);
+    for (int st = 0; st < CX_STAGES; st++) {
+      for (int l = 0; l < CX_LPS; l++) {
+        const CodecLayerW &L = cw.L[st][l];
+        const std::string p =
+            P + "decoder_blocks." + std::to_string(1 + 2 * st) + ".layers." + std::to_string(l) + ".";
+        add_slot(e, p + "attention_norm.weight", L.attn_norm, {cd}, true);
+        add_slot(e, p + "attention.q_norm.weight", L.q_norm, {cd}, true);
+        add_slot(e, p + "attention.k_norm.weight", L.k_norm, {cd}, true);
+        add_slot(e, p + "attention.wq.weight", L.wqkv, {cd, cd}, false);
+        add_slot(e, p + "attention.wk.weight", L.wqkv + (size_t)CD * CD, {cd, cd}, false);
+        add_slot(e, p + "attention.wv.weight", L.wqkv + (size_t)2 * CD * CD, {cd, cd}, false);
+        add_slot(e, p + "attention.wo.weight", L.wo, {cd, cd}, false);
+        add_slot(e, p + "attention_scale", L.attn_scale, {cd}, true);
+        add_slot(e, p + "ffn_norm.weight", L.ffn_norm, {cd}, true);
+        add_slot(e, p + "feed_forward.w1.weight", L.w13, {hid, cd}, false);
+        add_slot(e, p + "feed_forward.w3.weight", L.w13 + (size_t)CHID * CD, {hid, cd}, false);
+        add_slot(e, p + "feed_forward.w2.weight", L.w2, {cd, hid}, false);
+        add_slot(e, p + "ffn_scale", L.ffn_scale, {cd}, true);
+      }
+      if (st < CX_STAGES - 1) {
+        const std::string b =
+            P + "decoder_blocks." + std::to_string(2 + 2 * st) + ".conv.parametrizations.weight.";
+        add_slot(e, b + "original1", cw.up_w[st], {cd, cd, CK_UP}, false);
+        add_slot(e, b + "original0", cw.up_g[st], {cd, 1, 1}, true);
+      }
+    }
+    add_slot(e, P + "output_proj.conv.parametrizations.weight.original1", cw.out_w,
+             {CPATCH, cd, CK_OUT}, false);
+    add_slot(e, P + "output_proj.conv.parametrizations.weight.original0", cw.out_g, {CPATCH, 1, 1},
+             true);
+    add_slot(e, P + "quantizer.semantic_codebook.embedding_sum", cw.cb_sum, {CSEM, CSEMD}, false);
+    add_slot(e, P + "quantizer.semantic_codebook.cluster_usage", cw.cb_usage, {CSEM}, true);
+
+    // derived operands
+    std::vector<std::pair<void **, size_t>> parts = {
+        {(void **)&e->cx_cb, (size_t)CSEM * CSEMD * 2},
+        {(void **)&e->cx_ain, (size_t)CD * CKIN * 2},
+        {(void **)&e->cx_aout, (size_t)CPATCH_ROWS * CKOUT * 2},
+        {(void **)&e->cx_rs_in, (size_t)CD * 4},
+        {(void **)&e->cx_rs_out, (size_t)CPATCH_ROWS * 4}};
+    for (int st = 0; st < CX_STAGES - 1; st++) {
+      parts.push_back({(void **)&e->cx_aup[st], (size_t)2 * CD * CKUP * 2});
+      parts.push_back({(void **)&e->cx_s_up[st], (size_t)CD * 4});
+    }
+    size_t tot = 0;
+    for (auto &q : parts) tot += align256(q.second);
+    if (hipMalloc(&e->cx_parena, tot) != hipSuccess) {
+      vx_destroy(e);
+      return fail(nullptr, VX_E_NOMEM, "hipMalloc of %zu codec operand bytes failed", tot);
+    }
+    char *p = (char *)e->cx_parena;
+    for (auto &q : parts) {
+      *q.first = p;
+      p += align256(q.second);
+    }
+    if (const char *ch = getenv("VX_CODEC_CHUNK")) {  // tokens per codec GEMM (tuning, tests)
+      const int v = atoi(ch);
+      if (v >= 128 && v <= CX_MAXT && v % 128 == 0) e->cx_chunk = v;
+    }
+  }
 
   // ---- batched prefill buffers (one chunk of PF_MAXT tokens)
   {
@@ -778,6 +914,8 @@ void vx_destroy(vx_engine *e) {
   if (e->kv) (void)hipFree(e->kv);
   if (e->fm_parena) (void)hipFree(e->fm_parena);
   if (e->pf_arena) (void)hipFree(e->pf_arena);
+  if (e->cx_parena) (void)hipFree(e->cx_parena);
+  if (e->cx_arena) (void)hipFree(e->cx_arena);
   if (e->aarena) (void)hipFree(e->aarena);
   if (e->ev0) (void)hipEventDestroy(e->ev0);
   if (e->ev1) (void)hipEventDestroy(e->ev1);
@@ -803,6 +941,7 @@ int vx_load_tensor(vx_engine *e, const char *name, const uint16_t *f16, size_t n
   s.loaded = true;
   if (s.ptr == e->fm_time) e->tproj_ready = false;
   e->fm_packed_ready = false;
+  e->codec_ready = false;
   return VX_OK;
 }
 
@@ -843,10 +982,9 @@ int vx_load_safetensors(vx_engine *e, const char *path, int32_t *n_loaded, int32
   std::vector<std::pair<const std::string *, Slot *>> work;
   int skipped = 0;
   for (auto &kv : entries) {
-    const char *comp = st_component(kv.first);
     auto it = e->slots.find(kv.first);
-    if (!strcmp(comp, "other") || !strcmp(comp, "codec") || it == e->slots.end()) {
-      skipped++;  // codec decoder weights and names the engine does not use
+    if (!strcmp(st_component(kv.first), "other") || it == e->slots.end()) {
+      skipped++;  // names the engine does not use (codec tensors when it has no codec)
       continue;
     }
     const StEntry &t = kv.second;
@@ -896,8 +1034,7 @@ int vx_load_safetensors(vx_engine *e, const char *path, int32_t *n_loaded, int32
     }
     w.second->loaded = true;
   }
-  e->tproj_ready = false;
-  e->fm_packed_ready = false;
+  e->weights_changed();
   if (n_loaded) *n_loaded = (int32_t)work.size();
   if (n_skipped) *n_skipped = skipped;
   return VX_OK;
@@ -914,8 +1051,7 @@ int vx_init_synthetic(vx_engine *e, uint64_t seed, float std) {
   }
   LAUNCHCHK(e);
   HIPCHK(e, hipStreamSynchronize(e->st));
-  e->tproj_ready = false;
-  e->fm_packed_ready = false;
+  e->weights_changed();
   return VX_OK;
 }
 
@@ -1368,14 +1504,251 @@ void vx_generate_options_default(vx_generate_options *o) {
   o->ignore_eos = 0;
 }
 
+// -------------------------------------------------------- codec decoder
+// codecDecode (src/engine.ts:1402-1713) on MFMA GEMMs (vx_codec.h).
+
+// derived operands, rebuilt after any weight change: the normalised VQ
+// codebook (normalizeVQCodebook :593-613), the transposed convs' weight-norm
+// scales (precomputeConvTransposeScales :621-657), the causal convs' row
+// scales, and every conv weight in its GEMM order
+static int codec_prepare(vx_engine *e) {
+  if (e->codec_ready) return VX_OK;
+  const CodecW &w = e->cw;
+  hipStream_t st = e->st;
+  hipLaunchKernelGGL(cx_vq_norm_kernel, dim3(1024), dim3(256), 0, st, w.cb_sum, w.cb_usage, e->cx_cb);
+  hipLaunchKernelGGL(cx_conv_rowscale_kernel, dim3(CD / 64), dim3(64), 0, st, w.in_w, w.in_g, CD,
+                     CIN * CK_IN, CD, e->cx_rs_in);
+  hipLaunchKernelGGL(cx_conv_rowscale_kernel, dim3(CPATCH_ROWS / 64), dim3(64), 0, st, w.out_w,
+                     w.out_g, CPATCH, CKOUT, CPATCH_ROWS, e->cx_rs_out);
+  hipLaunchKernelGGL(cx_reorder_in_kernel, dim3(1024), dim3(256), 0, st, w.in_w, e->cx_ain);
+  hipLaunchKernelGGL(cx_reorder_out_kernel, dim3(1024), dim3(256), 0, st, w.out_w, e->cx_aout);
+  for (int s = 0; s < CX_STAGES - 1; s++) {
+    hipLaunchKernelGGL(cx_up_scale_kernel, dim3(CD), dim3(256), 0, st, w.up_w[s], w.up_g[s],
+                       e->cx_s_up[s]);
+    hipLaunchKernelGGL(cx_reorder_up_kernel, dim3(2048), dim3(256), 0, st, w.up_w[s], e->cx_aup[s]);
+  }
+  LAUNCHCHK(e);
+  HIPCHK(e, hipStreamSynchronize(st));
+  e->codec_ready = true;
+  return VX_OK;
+}
+
+// per-decode buffers for up to T frames (8 T tokens after the upsampling)
+static int codec_reserve(vx_engine *e, int T) {
+  if (T <= e->cx_cap) return VX_OK;
+  if (e->cx_arena) {
+    HIPCHK(e, hipStreamSynchronize(e->st));
+    HIPCHK(e, hipFree(e->cx_arena));
+    e->cx_arena = nullptr;
+    e->cx_cap = 0;
+  }
+  const size_t TT = (size_t)8 * T;
+  std::vector<std::pair<void **, size_t>> parts = {
+      {(void **)&e->cx_x, TT * CD * 4},
+      {(void **)&e->cx_x2, TT * CD * 4},
+      {(void **)&e->cx_q, TT * CD * 4},
+      {(void **)&e->cx_k, TT * CD * 4},
+      {(void **)&e->cx_v, TT * CD * 4},
+      {(void **)&e->cx_attn, TT * CD * 4},
+      {(void **)&e->cx_audio, TT * CPATCH * 4},
+      {(void **)&e->cx_c, CX_CCAP * 4},
+      {(void **)&e->cx_b, (size_t)CKOUT / 8 * CX_NC * 16},
+      {(void **)&e->cx_sem, (size_t)T * 4},
+      {(void **)&e->cx_ac, (size_t)T * NAC * 4}};
+  size_t tot = 0;
+  for (auto &q : parts) tot += align256(q.second);
+  if (hipMalloc(&e->cx_arena, tot) != hipSuccess)
+    return fail(e, VX_E_NOMEM, "hipMalloc of %zu codec bytes for %d frames failed", tot, T);
+  char *p = (char *)e->cx_arena;
+  for (auto &q : parts) {
+    *q.first = p;
+    p += align256(q.second);
+  }
+  e->cx_cap = T;
+  return VX_OK;
+}
+
+// C[S][nc][M] = A[M][K] x B[K][nc] with a k split S that fills the chip
+// (>= 256 blocks) while the slabs fit the output buffer; returns S
+extern "C++" {
+template <int K>
+static int cx_gemm_k(vx_engine *e, const uint16_t *A, int M, int nc) {
+  const int blocks = (M / PF_BM) * (nc / PF_BN);
+  int S = 1;
+  while (S < 8 && blocks * S < 256 && (K / 32) % (2 * S) == 0 &&
+         (size_t)2 * S * nc * M <= CX_CCAP)
+    S *= 2;
+  hipLaunchKernelGGL(pf_gemm_kernel<K>, dim3(M / PF_BM, nc / PF_BN, S), dim3(256), 0, e->st, A,
+                     e->cx_b, e->cx_c, M, nc);
+  return S;
+}
+}  // extern "C++"
+
+static int cx_gemm(vx_engine *e, int K, const uint16_t *A, int M, int nc) {
+  switch (K) {
+    case CKIN: return cx_gemm_k<CKIN>(e, A, M, nc);
+    case CD: return cx_gemm_k<CD>(e, A, M, nc);
+    case CKUP: return cx_gemm_k<CKUP>(e, A, M, nc);
+    case CHID: return cx_gemm_k<CHID>(e, A, M, nc);
+    default: return cx_gemm_k<CKOUT>(e, A, M, nc);
+  }
+}
+
+// the intermediates of debugCodecDecode (src/engine.ts:1719-1985)
+static int cx_stop_frames(int T, int stop) {
+  if (stop <= VX_CODEC_STOP_STAGE0) return T;
+  if (stop == VX_CODEC_STOP_AUDIO) return 8 * T;
+  const int s = (stop - VX_CODEC_STOP_STAGE0) / 2, up = (stop - VX_CODEC_STOP_STAGE0) % 2;
+  return T << (s + up);
+}
+
+// codes already in cx_sem / cx_ac; enqueues the decoder up to `stop` and
+// leaves the result in *res (device) with *count floats
+static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *count) {
+  hipStream_t st = e->st;
+  const CodecW &w = e->cw;
+  const int levels = e->cfg.acoustic_levels;
+  const dim3 blk(256);
+  // token chunks [t0, t0 + n) with nc = 2 * round_up(n, 128) B columns
+  auto chunks = [&](int TT, auto &&body) {
+    for (int t0 = 0; t0 < TT; t0 += e->cx_chunk) {
+      const int n = std::min(e->cx_chunk, TT - t0), nc = 2 * ((n + 127) / 128 * 128);
+      body(t0, n, nc);
+    }
+  };
+  if (stop == VX_CODEC_STOP_CONCAT) {
+    hipLaunchKernelGGL(cx_concat_kernel, dim3((T * CIN + 255) / 256), blk, 0, st, e->cx_cb,
+                       e->cx_sem, e->cx_ac, levels, T, e->cx_x);
+    *res = e->cx_x;
+    *count = (size_t)T * CIN;
+    return VX_OK;
+  }
+  // input conv: CausalConv1d(292 -> 1024, k = 3)
+  chunks(T, [&](int t0, int n, int nc) {
+    hipLaunchKernelGGL(cx_pack_in_kernel, dim3(nc / 2), dim3(128), 0, st, e->cx_cb, e->cx_sem,
+                       e->cx_ac, levels, t0, n, nc, e->cx_b);
+    const int S = cx_gemm(e, CKIN, e->cx_ain, CD, nc);
+    hipLaunchKernelGGL(cx_scale_rows_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, CD, nc, S,
+                       t0, e->cx_rs_in, CD, e->cx_x, CD);
+  });
+  int TT = T, at = VX_CODEC_STOP_INPUT_CONV;
+  float *x = e->cx_x, *x2 = e->cx_x2;
+  static const int kWindow[CX_STAGES] = {2, 4, 8, 16};  // src/engine.ts:1507
+  for (int s = 0; s < CX_STAGES && at < stop; s++) {
+    for (int l = 0; l < CX_LPS; l++) {
+      const CodecLayerW &L = w.L[s][l];
+      chunks(TT, [&](int t0, int n, int nc) {
+        hipLaunchKernelGGL(cx_pack_kernel<true>, dim3(nc / 2), blk, 0, st, x, CD, t0, n, nc,
+                           L.attn_norm, CX_NORM_EPS, e->cx_b);
+        const int S = cx_gemm(e, CD, L.wqkv, 3 * CD, nc);
+        hipLaunchKernelGGL(cx_qkv_epi_kernel, dim3(n, 3 * CNH / 4), blk, 0, st, e->cx_c, nc, S, t0,
+                           L.q_norm, L.k_norm, e->cx_q, e->cx_k, e->cx_v);
+      });
+      hipLaunchKernelGGL(cx_attn_kernel, dim3(TT, CNH / 4), blk, 0, st, e->cx_q, e->cx_k, e->cx_v,
+                         kWindow[s], e->cx_attn);
+      chunks(TT, [&](int t0, int n, int nc) {
+        hipLaunchKernelGGL(cx_pack_kernel<false>, dim3(nc / 2), blk, 0, st, e->cx_attn, CD, t0, n,
+                           nc, nullptr, 0.f, e->cx_b);
+        const int S = cx_gemm(e, CD, L.wo, CD, nc);
+        hipLaunchKernelGGL(cx_resid_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, S, t0,
+                           L.attn_scale, x);
+      });
+      chunks(TT, [&](int t0, int n, int nc) {
+        hipLaunchKernelGGL(cx_pack_kernel<true>, dim3(nc / 2), blk, 0, st, x, CD, t0, n, nc,
+                           L.ffn_norm, CX_NORM_EPS, e->cx_b);
+        int S = cx_gemm(e, CD, L.w13, 2 * CHID, nc);
+        // the gate/up GEMM has consumed B: the SwiGLU epilogue refills it
+        hipLaunchKernelGGL(cx_swiglu_epi_kernel, dim3(nc / 2, CHID / 8 / 256), blk, 0, st, e->cx_c,
+                           nc, S, n, e->cx_b);
+        S = cx_gemm(e, CHID, L.w2, CD, nc);
+        hipLaunchKernelGGL(cx_resid_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, S, t0,
+                           L.ffn_scale, x);
+      });
+    }
+    at = VX_CODEC_STOP_STAGE0 + 2 * s;
+    if (at == stop || s == CX_STAGES - 1) break;
+    // ConvTranspose1d(1024 -> 1024, k = 4, stride 2), output trimmed to 2 TT
+    chunks(TT, [&](int t0, int n, int nc) {
+      hipLaunchKernelGGL(cx_pack_up_kernel, dim3(nc / 2), blk, 0, st, x, e->cx_s_up[s], t0, n, nc,
+                         e->cx_b);
+      const int S = cx_gemm(e, CKUP, e->cx_aup[s], 2 * CD, nc);
+      hipLaunchKernelGGL(cx_up_epi_kernel, dim3(n, 2 * CD / 256), blk, 0, st, e->cx_c, nc, S, t0, x2);
+    });
+    std::swap(x, x2);
+    TT *= 2;
+    at = VX_CODEC_STOP_STAGE0 + 2 * s + 1;
+  }
+  if (stop != VX_CODEC_STOP_AUDIO) {
+    *res = x;
+    *count = (size_t)TT * CD;
+    return VX_OK;
+  }
+  // output conv: CausalConv1d(1024 -> 240, k = 7); step t gives samples
+  // [240 t, 240 t + 240)
+  chunks(TT, [&](int t0, int n, int nc) {
+    hipLaunchKernelGGL(cx_pack_out_kernel, dim3(nc / 2), blk, 0, st, x, t0, n, nc, e->cx_b);
+    const int S = cx_gemm(e, CKOUT, e->cx_aout, CPATCH_ROWS, nc);
+    hipLaunchKernelGGL(cx_scale_rows_epi_kernel, dim3(n, 1), blk, 0, st, e->cx_c, CPATCH_ROWS, nc,
+                       S, t0, e->cx_rs_out, CPATCH, e->cx_audio, CPATCH);
+  });
+  *res = e->cx_audio;
+  *count = (size_t)TT * CPATCH;
+  return VX_OK;
+}
+
+static int codec_decode_impl(vx_engine *e, const uint32_t *semantic, const uint32_t *acoustic,
+                             int32_t n_frames, int32_t stop, float *out, size_t out_count) {
+  if (!e) return VX_E_INVALID;
+  if (!e->codec_on) return fail(e, VX_E_STATE, "the engine was created without the codec decoder");
+  int rc = check_ready(e);
+  if (rc) return fail(e, VX_E_STATE, "Engine not initialized. Call init() and loadWeights() first.");
+  if (n_frames < 1 || n_frames > VX_CODEC_MAX_FRAMES || !semantic || !acoustic || !out ||
+      stop < VX_CODEC_STOP_CONCAT || stop > VX_CODEC_STOP_AUDIO)
+    return fail(e, VX_E_INVALID, "bad codec arguments (frames %d, stop %d)", n_frames, stop);
+  if (out_count < vx_codec_stop_count(n_frames, stop))
+    return fail(e, VX_E_INVALID, "output holds %zu floats, %zu needed", out_count,
+                vx_codec_stop_count(n_frames, stop));
+  if ((rc = codec_prepare(e)) || (rc = codec_reserve(e, n_frames))) return rc;
+  HIPCHK(e, hipMemcpyAsync(e->cx_sem, semantic, (size_t)n_frames * 4, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipMemcpyAsync(e->cx_ac, acoustic, (size_t)n_frames * NAC * 4, hipMemcpyHostToDevice,
+                           e->st));
+  const float *res = nullptr;
+  size_t count = 0;
+  if ((rc = codec_run(e, n_frames, stop, &res, &count))) return rc;
+  LAUNCHCHK(e);
+  HIPCHK(e, hipMemcpyAsync(out, res, count * 4, hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+size_t vx_codec_stop_count(int32_t n_frames, int32_t stop) {
+  if (n_frames < 0 || stop < VX_CODEC_STOP_CONCAT || stop > VX_CODEC_STOP_AUDIO) return 0;
+  const size_t f = (size_t)cx_stop_frames(n_frames, stop);
+  return f * (stop == VX_CODEC_STOP_CONCAT ? CIN : stop == VX_CODEC_STOP_AUDIO ? CPATCH : CD);
+}
+
+int vx_codec_decode(vx_engine *e, const uint32_t *semantic, const uint32_t *acoustic,
+                    int32_t n_frames, float *audio) {
+  return codec_decode_impl(e, semantic, acoustic, n_frames, VX_CODEC_STOP_AUDIO, audio,
+                           vx_codec_stop_count(n_frames, VX_CODEC_STOP_AUDIO));
+}
+
+int vx_codec_decode_debug(vx_engine *e, const uint32_t *semantic, const uint32_t *acoustic,
+                          int32_t n_frames, int32_t stop, float *out, size_t out_count) {
+  return codec_decode_impl(e, semantic, acoustic, n_frames, stop, out, out_count);
+}
+
 // sampleTopP, src/engine.ts:247-289, with a seeded uniform in place of
 // Math.random.  Float32Array intermediates, double accumulators, stable
 // descending sort, as the TypeScript does.
 int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t audio_start,
                 int32_t audio_count, const float *voice, int32_t max_frames,
                 const vx_generate_options *opt_in, vx_frame_cb on_frame, vx_stage_cb on_stage,
-                void *user, uint32_t *sem_out, uint32_t *ac_out, vx_generate_stats *stats) {
+                void *user, uint32_t *sem_out, uint32_t *ac_out, float *audio_out,
+                vx_generate_stats *stats) {
   if (!e) return VX_E_INVALID;
+  if (audio_out && !e->codec_on)
+    return fail(e, VX_E_STATE, "the engine was created without the codec decoder");
   int rc = check_ready(e);
   if (rc) return fail(e, VX_E_STATE, "Engine not initialized. Call init() and loadWeights() first.");
   if (n_tokens < 0 || (n_tokens > 0 && !tokens) || max_frames < 0)
@@ -1390,6 +1763,11 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
     return std::chrono::duration<double, std::milli>(b - a).count();
   };
   if ((rc = vx_reset(e))) return rc;
+  std::vector<uint32_t> sem_v, ac_v;  // the codes, for the codec decode
+  if (audio_out) {
+    sem_v.reserve(max_frames);
+    ac_v.reserve((size_t)max_frames * NAC);
+  }
   HIPCHK(e, hipMemcpyAsync(e->noise_seed, &opt.seed, 8, hipMemcpyHostToDevice, e->st));
   HIPCHK(e, hipStreamSynchronize(e->st));
   auto t0 = clk::now();
@@ -1439,6 +1817,10 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
       HIPCHK(e, hipStreamSynchronize(e->st));
       if (sem_out) sem_out[f] = code;
       if (ac_out) memcpy(ac_out + (size_t)f * NAC, codes, sizeof codes);
+      if (audio_out) {
+        sem_v.push_back(code);
+        ac_v.insert(ac_v.end(), codes, codes + NAC);
+      }
       frames++;
       if (on_frame) on_frame(user, f, code, codes);
     }
@@ -1484,21 +1866,31 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
       }
       if (sem_out) sem_out[f] = code;
       if (ac_out) memcpy(ac_out + (size_t)f * NAC, codes, sizeof codes);
+      if (audio_out) {
+        sem_v.push_back(code);
+        ac_v.insert(ac_v.end(), codes, codes + NAC);
+      }
       frames++;
       if (on_frame) on_frame(user, f, code, codes);
     }
   }
+  HIPCHK(e, hipStreamSynchronize(e->st));
   auto t2 = clk::now();
   if (on_stage) {
     on_stage(user, 1, ms(t1, t2));
     on_stage(user, 2, -1.0);
-    on_stage(user, 2, 0.0);
   }
+  // codec decode of all frames (src/engine.ts:2588-2599)
+  if (audio_out && frames > 0 &&
+      (rc = vx_codec_decode(e, sem_v.data(), ac_v.data(), frames, audio_out)))
+    return rc;
+  auto t3 = clk::now();
+  if (on_stage) on_stage(user, 2, ms(t2, t3));
   if (stats) {
     stats->backbone_ms = ms(t0, t1);
     stats->fm_ms = ms(t1, t2);
-    stats->codec_ms = 0;
-    stats->total_ms = ms(t0, t2);
+    stats->codec_ms = ms(t2, t3);
+    stats->total_ms = ms(t0, t3);
     stats->frames_generated = frames;
   }
   HIPCHK(e, hipStreamSynchronize(e->st));

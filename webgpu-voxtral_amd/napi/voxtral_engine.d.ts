@@ -10,6 +10,8 @@ export interface VoxtralConfig {
   fm?: { n_layers?: number; nfe?: number; cfg_alpha?: number };
   /** KV cache element type: false f32 (the reference's), true f16 */
   kvF16?: boolean;
+  /** false: no codec decoder (generate() returns empty audio) */
+  codec?: boolean;
 }
 
 export interface EngineOptions {
@@ -20,7 +22,7 @@ export interface EngineOptions {
 export interface TTSResult {
   semanticCodes: number[];
   acousticCodes: number[][];
-  /** empty: the codec decoder is outside this library */
+  /** codecDecode of the generated frames: 1920 samples of 24 kHz audio each */
   audio: Float32Array;
   stats: {
     backboneMs: number;
@@ -62,6 +64,8 @@ export declare class VoxtralEngine {
     x_final: Float32Array;
   }>;
   fmStepAndRead(): Promise<Uint32Array>;
+  codecDecode(semanticCodes: ArrayLike<number>, acousticCodes: ArrayLike<number>): Promise<Float32Array>;
+  debugCodecDecode(semanticCodes: ArrayLike<number>, acousticCodes: ArrayLike<number>): Promise<Record<string, Float32Array>>;
   generate(
     tokens: number[],
     audioTokenStart: number,

@@ -14,6 +14,13 @@ const EMBED_TOKEN = 0;
 const EMBED_AUDIO = 1;
 const EMBED_PRECOMPUTED = 2;
 
+// debugCodecDecode's intermediates in decoder order (VX_CODEC_STOP_* 0..9)
+const CODEC_STOPS = ['concat', 'after_input_conv',
+  'after_stage0_transformer', 'after_stage0_conv_up',
+  'after_stage1_transformer', 'after_stage1_conv_up',
+  'after_stage2_transformer', 'after_stage2_conv_up',
+  'after_stage3_transformer', 'audio'];
+
 // reference defaultConfig (src/types.ts:70-122), the fields the engine reads
 function flattenConfig(config) {
   if (!config) return null;
@@ -34,6 +41,7 @@ function flattenConfig(config) {
   put('nfe', fm.nfe);
   put('cfgAlpha', fm.cfg_alpha);
   put('kvF16', config.kvF16 ? 1 : undefined);
+  put('codec', config.codec === false ? 0 : undefined);
   return out;
 }
 
@@ -153,18 +161,43 @@ class VoxtralEngine {
 
   /**
    * generate(tokens, audioTokenStart, audioTokenCount, voiceEmbeddings,
-   * maxFrames = 500, onFrame?, onStage?), src/engine.ts:2416-2616.  The codec
-   * decoder is outside this library: `audio` is empty.  `options` (not in
-   * the reference) selects sampling 'top_p' (default, the reference's) or
-   * 'greedy', the seed that replaces Math.random, and ignoreEos.
+   * maxFrames = 500, onFrame?, onStage?), src/engine.ts:2416-2616.  `audio`
+   * is codecDecode of the generated frames (1920 samples each; empty for an
+   * engine created with config.codec === false).  `options` (not in the
+   * reference) selects sampling 'top_p' (default, the reference's),
+   * 'top_p_host' or 'greedy', the seed that replaces Math.random, and
+   * ignoreEos.
    */
   async generate(tokens, audioTokenStart, audioTokenCount, voiceEmbeddings, maxFrames,
     onFrame, onStage, options) {
-    const r = await native.generate(this._handle(), tokens, audioTokenStart, audioTokenCount,
-      voiceEmbeddings || null, maxFrames === undefined ? 500 : maxFrames, options || null,
+    const opts = Object.assign({}, options || {}, { audio: this._codec() });
+    return native.generate(this._handle(), tokens, audioTokenStart, audioTokenCount,
+      voiceEmbeddings || null, maxFrames === undefined ? 500 : maxFrames, opts,
       onFrame || null, onStage || null);
-    r.audio = new Float32Array(0);
-    return r;
+  }
+
+  /** codecDecode(semanticCodes, acousticCodes), src/engine.ts:1402-1713:
+   *  codes [T] and [T * 36] -> 24 kHz samples [T * 1920] */
+  async codecDecode(semanticCodes, acousticCodes) {
+    return native.codecDecode(this._handle(), Uint32Array.from(semanticCodes),
+      Uint32Array.from(acousticCodes));
+  }
+
+  /** debugCodecDecode, src/engine.ts:1719-1985: the decoder's intermediates
+   *  by the reference's names */
+  async debugCodecDecode(semanticCodes, acousticCodes) {
+    const sem = Uint32Array.from(semanticCodes);
+    const ac = Uint32Array.from(acousticCodes);
+    const out = {};
+    CODEC_STOPS.forEach((name, stop) => {
+      out[name] = native.codecDecode(this._handle(), sem, ac, stop);
+    });
+    out.after_output_conv = out.audio;
+    return out;
+  }
+
+  _codec() {
+    return !(this.config && this.config.codec === false);
   }
 
   /** destroy(), src/engine.ts:2621-2632 */

@@ -133,7 +133,8 @@ napi_value create(napi_env env, napi_callback_info info) {
                   {"fmLayers", &c.fm_layers, nullptr},
                   {"nfe", &c.nfe, nullptr},
                   {"cfgAlpha", nullptr, &c.cfg_alpha},
-                  {"kvF16", &c.kv_f16, nullptr}};
+                  {"kvF16", &c.kv_f16, nullptr},
+                  {"codec", &c.codec, nullptr}};
     for (auto &f : fields) {
       bool has = false;
       napi_has_named_property(env, a.v[0], f.k, &has);
@@ -202,6 +203,30 @@ napi_value load_safetensors(napi_env env, napi_callback_info info) {
   NAPI_OK(env, napi_create_int32(env, skipped, &x));
   NAPI_OK(env, napi_set_named_property(env, o, "skipped", x));
   return o;
+}
+
+// codecDecode(h, Uint32Array semantic, Uint32Array acoustic[, stop]) ->
+// Float32Array (stop: VX_CODEC_STOP_*, default the waveform)
+napi_value codec_decode(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a) || a.n < 3) return nullptr;
+  vx_engine *e = handle(env, a.v[0]);
+  if (!e) return nullptr;
+  size_t ns = 0, na = 0;
+  auto *sem = (const uint32_t *)typed(env, a.v[1], napi_uint32_array, &ns);
+  if (!sem) return nullptr;
+  auto *ac = (const uint32_t *)typed(env, a.v[2], napi_uint32_array, &na);
+  if (!ac) return nullptr;
+  if (na != ns * 36) {
+    napi_throw_range_error(env, nullptr, "acousticCodes must hold 36 codes per frame");
+    return nullptr;
+  }
+  const int32_t stop = a.n > 3 && !is_nullish(env, a.v[3]) ? (int32_t)num(env, a.v[3])
+                                                           : VX_CODEC_STOP_AUDIO;
+  std::vector<float> out(std::max<size_t>(vx_codec_stop_count((int32_t)ns, stop), 1));
+  int rc = vx_codec_decode_debug(e, sem, ac, (int32_t)ns, stop, out.data(), out.size());
+  if (rc) return throw_vx(env, e, rc);
+  return new_f32(env, out.data(), vx_codec_stop_count((int32_t)ns, stop));
 }
 
 napi_value init_synthetic(napi_env env, napi_callback_info info) {
@@ -357,6 +382,8 @@ struct GenJob {
   napi_ref on_frame = nullptr, on_stage = nullptr;
   napi_threadsafe_function events = nullptr;
   std::vector<uint32_t> sem, ac;
+  bool want_audio = false;
+  std::vector<float> audio;
   vx_generate_stats stats;
   int rc = 0;
   std::string err;
@@ -391,6 +418,8 @@ void settle(napi_env env, GenJob *j) {
   }
   napi_set_named_property(env, out, "semanticCodes", sem);
   napi_set_named_property(env, out, "acousticCodes", ac);
+  napi_set_named_property(env, out, "audio",
+                          new_f32(env, j->audio.data(), j->want_audio ? (size_t)n * VX_FRAME_SAMPLES : 0));
   napi_create_object(env, &stats);
   set_int(env, stats, "backboneMs", j->stats.backbone_ms);
   set_int(env, stats, "fmMs", j->stats.fm_ms);
@@ -460,9 +489,11 @@ void gen_execute(napi_env, void *data) {
   const int nf = j->max_frames > 0 ? j->max_frames : 1;
   j->sem.assign(nf, 0);
   j->ac.assign((size_t)nf * 36, 0);
+  if (j->want_audio) j->audio.assign((size_t)nf * VX_FRAME_SAMPLES, 0.f);
   j->rc = vx_generate(j->e, j->tokens.data(), (int32_t)j->tokens.size(), j->audio_start,
                       j->audio_count, j->has_voice ? j->voice.data() : nullptr, j->max_frames,
-                      &j->opt, frame_cb, stage_cb, j, j->sem.data(), j->ac.data(), &j->stats);
+                      &j->opt, frame_cb, stage_cb, j, j->sem.data(), j->ac.data(),
+                      j->want_audio ? j->audio.data() : nullptr, &j->stats);
   if (j->rc) j->err = vx_last_error(j->e);
 }
 
@@ -535,8 +566,8 @@ napi_value generate(napi_env env, napi_callback_info info) {
       j->opt.sampling = m == "greedy" ? VX_SAMPLE_GREEDY
                         : m == "top_p_host" ? VX_SAMPLE_TOP_P_HOST : VX_SAMPLE_TOP_P;
     }
-    const char *keys[] = {"topP", "temperature", "seed", "ignoreEos"};
-    for (int k = 0; k < 4; k++) {
+    const char *keys[] = {"topP", "temperature", "seed", "ignoreEos", "audio"};
+    for (int k = 0; k < 5; k++) {
       napi_has_named_property(env, a.v[6], keys[k], &has);
       if (!has) continue;
       napi_get_named_property(env, a.v[6], keys[k], &v);
@@ -554,6 +585,7 @@ napi_value generate(napi_env env, napi_callback_info info) {
       if (k == 1) j->opt.temperature = d;
       if (k == 2) j->opt.seed = (uint64_t)d;
       if (k == 3) j->opt.ignore_eos = d != 0;
+      if (k == 4) j->want_audio = d != 0;
     }
   }
   if (a.n > 7 && !is_nullish(env, a.v[7])) napi_create_reference(env, a.v[7], 1, &j->on_frame);
@@ -580,6 +612,7 @@ napi_value init(napi_env env, napi_value exports) {
              {"destroy", destroy},
              {"loadTensor", load_tensor},
              {"loadSafetensors", load_safetensors},
+             {"codecDecode", codec_decode},
              {"initSynthetic", init_synthetic},
              {"isReady", is_ready},
              {"reset", reset},

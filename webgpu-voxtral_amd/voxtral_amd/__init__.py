@@ -42,6 +42,7 @@ class Config(ctypes.Structure):
         ("n_acoustic_out", ctypes.c_int32), ("semantic_vocab", ctypes.c_int32),
         ("acoustic_levels", ctypes.c_int32), ("audio_vocab", ctypes.c_int32),
         ("kv_f16", ctypes.c_int32),  # KV cache element type: 0 f32 (reference), 1 f16
+        ("codec", ctypes.c_int32),   # 1: the codec decoder is part of the engine (default)
     ]
 
 
@@ -60,6 +61,15 @@ class GenerateStats(ctypes.Structure):
 FRAME_CB = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32,
                             ctypes.POINTER(ctypes.c_uint32))
 STAGE_CB = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int32, ctypes.c_double)
+
+FRAME_SAMPLES = 1920  # 80 ms of 24 kHz audio per frame (VX_FRAME_SAMPLES)
+NAC = 36
+# debugCodecDecode's intermediates in decoder order (VX_CODEC_STOP_* 0..9)
+CODEC_STOPS = ["concat", "after_input_conv",
+               "after_stage0_transformer", "after_stage0_conv_up",
+               "after_stage1_transformer", "after_stage1_conv_up",
+               "after_stage2_transformer", "after_stage2_conv_up",
+               "after_stage3_transformer", "audio"]
 
 _VP = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -94,7 +104,10 @@ _SIGS = {
     "vx_fill_kv_synthetic": (_I32, [_VP, ctypes.c_uint64, _I32]),
     "vx_generate_options_default": (None, [ctypes.POINTER(GenerateOptions)]),
     "vx_generate": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP, _I32, ctypes.POINTER(GenerateOptions),
-                           FRAME_CB, STAGE_CB, _VP, _VP, _VP, ctypes.POINTER(GenerateStats)]),
+                           FRAME_CB, STAGE_CB, _VP, _VP, _VP, _VP, ctypes.POINTER(GenerateStats)]),
+    "vx_codec_decode": (_I32, [_VP, _VP, _VP, _I32, _VP]),
+    "vx_codec_decode_debug": (_I32, [_VP, _VP, _VP, _I32, _I32, _VP, ctypes.c_size_t]),
+    "vx_codec_stop_count": (ctypes.c_size_t, [_I32, _I32]),
     "vx_time_backbone_steps": (_I32, [_VP, _I32, _I32, ctypes.POINTER(ctypes.c_float)]),
     "vx_time_frames": (_I32, [_VP, _I32, ctypes.POINTER(ctypes.c_float)]),
     "vx_time_kernel": (_I32, [_VP, _I32, _I32, ctypes.POINTER(ctypes.c_float),
@@ -372,6 +385,7 @@ class VoxtralEngine:
         opt.top_p, opt.temperature, opt.seed, opt.ignore_eos = top_p, temperature, seed, int(ignore_eos)
         sem = np.zeros(max(1, max_frames), np.uint32)
         ac = np.zeros((max(1, max_frames), 36), np.uint32)
+        audio = np.zeros(max(1, max_frames) * FRAME_SAMPLES, np.float32) if self.config.codec else None
         stages = ["backbone", "fm", "codec"]
 
         def _frame(user, f, s, codes):
@@ -387,16 +401,49 @@ class VoxtralEngine:
         self._check(self._lib.vx_generate(self._h, toks.ctypes.data, toks.size, audio_token_start,
                                           audio_token_count, _ptr(voice), max_frames,
                                           ctypes.byref(opt), fcb, scb, None, sem.ctypes.data,
-                                          ac.ctypes.data, ctypes.byref(stats)))
+                                          ac.ctypes.data, _ptr(audio), ctypes.byref(stats)))
         n = stats.frames_generated
         return {
             "semanticCodes": [int(v) for v in sem[:n]],
             "acousticCodes": [list(map(int, r)) for r in ac[:n]],
-            "audio": np.zeros(0, np.float32),  # codec decoder is outside this library
+            # codecDecode of the frames (empty for an engine without the codec)
+            "audio": audio[:n * FRAME_SAMPLES].copy() if audio is not None else np.zeros(0, np.float32),
             "stats": {"backboneMs": stats.backbone_ms, "fmMs": stats.fm_ms,
                       "codecMs": stats.codec_ms, "totalMs": stats.total_ms,
                       "framesGenerated": n},
         }
+
+    # -- codec decoder (:1402-1985) --
+    def _codes(self, semantic, acoustic):
+        sem = np.ascontiguousarray(semantic, np.uint32).ravel()
+        ac = np.ascontiguousarray(acoustic, np.uint32).ravel()
+        if ac.size != NAC * sem.size:
+            raise ValueError("acousticCodes must hold 36 codes per frame")
+        return sem, ac
+
+    def codec_decode(self, semantic_codes, acoustic_codes):
+        """codecDecode (:1402-1713): codes [T], [T][36] -> 24 kHz samples [T * 1920]."""
+        sem, ac = self._codes(semantic_codes, acoustic_codes)
+        out = np.empty(max(1, sem.size * FRAME_SAMPLES), np.float32)
+        self._check(self._lib.vx_codec_decode(self._h, sem.ctypes.data, ac.ctypes.data, sem.size,
+                                              out.ctypes.data))
+        return out[:sem.size * FRAME_SAMPLES]
+
+    def codec_decode_to(self, semantic_codes, acoustic_codes, stop):
+        """The decoder up to one intermediate of debugCodecDecode (CODEC_STOPS)."""
+        sem, ac = self._codes(semantic_codes, acoustic_codes)
+        k = CODEC_STOPS.index(stop)
+        n = self._lib.vx_codec_stop_count(sem.size, k)
+        out = np.empty(max(1, n), np.float32)
+        self._check(self._lib.vx_codec_decode_debug(self._h, sem.ctypes.data, ac.ctypes.data,
+                                                    sem.size, k, out.ctypes.data, out.size))
+        return out[:n]
+
+    def debug_codec_decode(self, semantic_codes, acoustic_codes):
+        """debugCodecDecode (:1719-1985): every intermediate by name."""
+        out = {name: self.codec_decode_to(semantic_codes, acoustic_codes, name) for name in CODEC_STOPS}
+        out["after_output_conv"] = out["audio"]
+        return out
 
     def sample_top_p(self, logits, valid, top_p, temperature, state, on_device=True):
         """sampleTopP (src/engine.ts:247-289) on caller logits with indices 0
