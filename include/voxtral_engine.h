@@ -238,6 +238,29 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens,
                 uint32_t *semantic_out, uint32_t *acoustic_out, float *audio_out,
                 vx_generate_stats *stats);
 
+/* ----------------------------------------------------------- tokenizer */
+/* Byte-level BPE of TekkenTokenizer (src/tokenizer.ts:58-249), encoding
+ * only.  Pre-tokenisation (the tekken.json regex pattern) stays with the
+ * host's regex engine; the merge loop runs here.  Errors are reported
+ * through vx_last_error(NULL). */
+typedef struct vx_tokenizer vx_tokenizer;
+
+/* constructor, src/tokenizer.ts:66-96: vocabulary entry i is the byte
+ * string blob[offsets[i] .. offsets[i + 1]) (decoded token_bytes) with its
+ * rank; token id = rank + num_special (default_num_special_tokens). */
+int vx_tokenizer_create(const uint8_t *blob, const int64_t *offsets, const int32_t *ranks,
+                        int32_t n, int32_t num_special, vx_tokenizer **out);
+void vx_tokenizer_destroy(vx_tokenizer *t);
+
+/* encode + bpeEncode over pre-tokenized pieces (src/tokenizer.ts:176-249): piece j
+ * is the UTF-8 byte string bytes[offsets[j] .. offsets[j + 1]).  The ids of
+ * all pieces, in order, go to out[0 .. *n_out); VX_E_RANGE (with *n_out
+ * set) when cap is too small.  A part missing from the vocabulary encodes
+ * as 0 (UNK), an empty piece as one UNK, as in the reference. */
+int vx_tokenizer_encode_pieces(const vx_tokenizer *t, const uint8_t *bytes,
+                               const int64_t *offsets, int32_t n_pieces, int32_t *out,
+                               int64_t cap, int64_t *n_out);
+
 /* ------------------------------------------------------- codec decoder */
 #define VX_FRAME_SAMPLES 1920     /* 80 ms of 24 kHz audio per frame */
 #define VX_CODEC_MAX_FRAMES 65536 /* 87 minutes of audio per call */

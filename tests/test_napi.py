@@ -38,6 +38,7 @@ e.init().then(() => console.log(JSON.stringify({{names, ready, msg, init: 'ok'}}
 """)
     r = json.loads(out.strip().splitlines()[-1])
     assert r["names"] == sorted(["create", "destroy", "loadTensor", "loadSafetensors", "codecDecode",
+                                 "tokenizerCreate", "tokenizerEncode",
                                  "initSynthetic", "isReady",
                                  "reset", "position", "backboneStep", "fmForward",
                                  "setSemanticCode", "read", "generate"])

@@ -21,6 +21,7 @@
 #include "vx_prefill.h"
 #include "vx_codec.h"
 #include "vx_loader.h"
+#include "vx_tokenizer.h"
 
 #include <fcntl.h>
 #include <unistd.h>
@@ -64,6 +65,10 @@ constexpr uint64_t kNoiseStream = 0x45237962ac6f43f0ull;
 constexpr size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 }  // namespace
+
+struct vx_tokenizer {
+  vx::BpeVocab vocab;
+};
 
 struct vx_engine {
   vx_config cfg;
@@ -1894,6 +1899,46 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
     stats->frames_generated = frames;
   }
   HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+// ------------------------------------------------------------ tokenizer
+int vx_tokenizer_create(const uint8_t *blob, const int64_t *offsets, const int32_t *ranks,
+                        int32_t n, int32_t num_special, vx_tokenizer **out) {
+  if (!out) return fail(nullptr, VX_E_INVALID, "out is NULL");
+  *out = nullptr;
+  if (n < 0 || (n > 0 && (!blob || !offsets || !ranks)) || num_special < 0)
+    return fail(nullptr, VX_E_INVALID, "bad tokenizer vocabulary arguments");
+  auto *t = new vx_tokenizer{BpeVocab(num_special)};
+  for (int32_t i = 0; i < n; i++) {
+    if (offsets[i] < 0 || offsets[i + 1] < offsets[i] || ranks[i] < 0) {
+      delete t;
+      return fail(nullptr, VX_E_INVALID, "vocabulary entry %d is malformed", i);
+    }
+    t->vocab.add(blob + offsets[i], (size_t)(offsets[i + 1] - offsets[i]), ranks[i]);
+  }
+  *out = t;
+  return VX_OK;
+}
+
+void vx_tokenizer_destroy(vx_tokenizer *t) { delete t; }
+
+int vx_tokenizer_encode_pieces(const vx_tokenizer *t, const uint8_t *bytes,
+                               const int64_t *offsets, int32_t n_pieces, int32_t *out, int64_t cap,
+                               int64_t *n_out) {
+  if (!t || n_pieces < 0 || (n_pieces > 0 && (!bytes || !offsets)) || !n_out || cap < 0 ||
+      (cap > 0 && !out))
+    return fail(nullptr, VX_E_INVALID, "bad tokenizer arguments");
+  std::vector<int32_t> ids;
+  for (int32_t j = 0; j < n_pieces; j++) {
+    if (offsets[j] < 0 || offsets[j + 1] < offsets[j])
+      return fail(nullptr, VX_E_INVALID, "piece %d is malformed", j);
+    t->vocab.encode(bytes + offsets[j], (size_t)(offsets[j + 1] - offsets[j]), ids);
+  }
+  *n_out = (int64_t)ids.size();
+  if ((int64_t)ids.size() > cap)
+    return fail(nullptr, VX_E_RANGE, "%zu token ids, room for %lld", ids.size(), (long long)cap);
+  std::copy(ids.begin(), ids.end(), out);
   return VX_OK;
 }
 

@@ -229,6 +229,66 @@ napi_value codec_decode(napi_env env, napi_callback_info info) {
   return new_f32(env, out.data(), vx_codec_stop_count((int32_t)ns, stop));
 }
 
+// ------------------------------------------------------------ tokenizer
+void tokenizer_finalize(napi_env, void *data, void *) {
+  vx_tokenizer_destroy(static_cast<vx_tokenizer *>(data));
+}
+
+// tokenizerCreate(Uint8Array blob, Int32Array offsets[n + 1], Int32Array ranks[n],
+//                 numSpecial) -> external (freed with the JS object)
+napi_value tokenizer_create(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a) || a.n < 4) return nullptr;
+  size_t nb = 0, no = 0, nr = 0;
+  auto *blob = (const uint8_t *)typed(env, a.v[0], napi_uint8_array, &nb);
+  auto *off = (const int32_t *)typed(env, a.v[1], napi_int32_array, &no);
+  auto *ranks = (const int32_t *)typed(env, a.v[2], napi_int32_array, &nr);
+  if (!blob || !off || !ranks) return nullptr;
+  if (no != nr + 1 || (size_t)off[nr] > nb) {
+    napi_throw_range_error(env, nullptr, "tokenizer vocabulary arrays do not match");
+    return nullptr;
+  }
+  std::vector<int64_t> off64(off, off + no);
+  vx_tokenizer *t = nullptr;
+  int rc = vx_tokenizer_create(blob, off64.data(), ranks, (int32_t)nr, (int32_t)num(env, a.v[3]), &t);
+  if (rc) return throw_vx(env, nullptr, rc);
+  napi_value h;
+  NAPI_OK(env, napi_create_external(env, t, tokenizer_finalize, nullptr, &h));
+  return h;
+}
+
+// tokenizerEncode(handle, Uint8Array bytes, Int32Array offsets[n + 1]) -> Int32Array
+napi_value tokenizer_encode(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a) || a.n < 3) return nullptr;
+  void *p = nullptr;
+  if (napi_get_value_external(env, a.v[0], &p) != napi_ok || !p) {
+    napi_throw_type_error(env, nullptr, "not a tokenizer handle");
+    return nullptr;
+  }
+  size_t nb = 0, no = 0;
+  auto *bytes = (const uint8_t *)typed(env, a.v[1], napi_uint8_array, &nb);
+  auto *off = (const int32_t *)typed(env, a.v[2], napi_int32_array, &no);
+  if (!bytes || !off) return nullptr;
+  if (no < 1 || (size_t)off[no - 1] > nb) {
+    napi_throw_range_error(env, nullptr, "piece offsets do not match the bytes");
+    return nullptr;
+  }
+  std::vector<int64_t> off64(off, off + no);
+  const int64_t cap = (int64_t)nb + (int64_t)no;
+  std::vector<int32_t> ids((size_t)cap);
+  int64_t n = 0;
+  int rc = vx_tokenizer_encode_pieces(static_cast<vx_tokenizer *>(p), bytes, off64.data(),
+                                      (int32_t)(no - 1), ids.data(), cap, &n);
+  if (rc) return throw_vx(env, nullptr, rc);
+  napi_value ab, out;
+  void *dst = nullptr;
+  NAPI_OK(env, napi_create_arraybuffer(env, (size_t)n * 4, &dst, &ab));
+  if (n) memcpy(dst, ids.data(), (size_t)n * 4);
+  NAPI_OK(env, napi_create_typedarray(env, napi_int32_array, (size_t)n, ab, 0, &out));
+  return out;
+}
+
 napi_value init_synthetic(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a) || a.n < 3) return nullptr;
@@ -613,6 +673,8 @@ napi_value init(napi_env env, napi_value exports) {
              {"loadTensor", load_tensor},
              {"loadSafetensors", load_safetensors},
              {"codecDecode", codec_decode},
+             {"tokenizerCreate", tokenizer_create},
+             {"tokenizerEncode", tokenizer_encode},
              {"initSynthetic", init_synthetic},
              {"isReady", is_ready},
              {"reset", reset},

@@ -108,6 +108,10 @@ _SIGS = {
     "vx_codec_decode": (_I32, [_VP, _VP, _VP, _I32, _VP]),
     "vx_codec_decode_debug": (_I32, [_VP, _VP, _VP, _I32, _I32, _VP, ctypes.c_size_t]),
     "vx_codec_stop_count": (ctypes.c_size_t, [_I32, _I32]),
+    "vx_tokenizer_create": (_I32, [_VP, _VP, _VP, _I32, _I32, ctypes.POINTER(_VP)]),
+    "vx_tokenizer_destroy": (None, [_VP]),
+    "vx_tokenizer_encode_pieces": (_I32, [_VP, _VP, _VP, _I32, _VP, ctypes.c_int64,
+                                          ctypes.POINTER(ctypes.c_int64)]),
     "vx_time_backbone_steps": (_I32, [_VP, _I32, _I32, ctypes.POINTER(ctypes.c_float)]),
     "vx_time_frames": (_I32, [_VP, _I32, ctypes.POINTER(ctypes.c_float)]),
     "vx_time_kernel": (_I32, [_VP, _I32, _I32, ctypes.POINTER(ctypes.c_float),
