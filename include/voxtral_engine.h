@@ -284,7 +284,7 @@ int vx_codec_decode_debug(vx_engine *e, const uint32_t *semantic, const uint32_t
 size_t vx_codec_stop_count(int32_t n_frames, int32_t stop);
 
 /* sampleTopP on caller logits (test plumbing): logits f32[n] with indices
- * 0 and >= valid masked, n <= 16384.  *state: the splitmix64 state of the
+ * 0 and >= valid masked, n <= 9216.  *state: the splitmix64 state of the
  * uniform (advanced by one draw).  on_device != 0 runs the device kernel
  * used by generate(), else the host implementation. */
 int vx_sample_top_p(vx_engine *e, const float *logits, int32_t n, int32_t valid,

@@ -860,7 +860,7 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   aplace((void **)&e->noise_seed, 8);
   aplace((void **)&e->rng_state, 8);
   aplace((void **)&e->tp_params, 16);
-  aplace((void **)&e->tp_logits, (size_t)TP_N * 4);
+  aplace((void **)&e->tp_logits, (size_t)TP_MAXN * 4);
   aplace((void **)&e->fm_seq, 6 * DIM * 4);
   aplace((void **)&e->fm_q, 6 * QD * 4);
   aplace((void **)&e->fm_k, 6 * KVD * 4);
@@ -1477,7 +1477,7 @@ static uint32_t sample_top_p(const float *logits, int n, double top_p, double te
 int vx_sample_top_p(vx_engine *e, const float *logits, int32_t n, int32_t valid, double top_p,
                     double temperature, uint64_t *state, int32_t on_device, uint32_t *code) {
   if (!e || !logits || !state || !code) return VX_E_INVALID;
-  if (n < 2 || n > TP_N || valid < 2 || temperature <= 0.0)
+  if (n < 2 || n > TP_MAXN || valid < 2 || temperature <= 0.0)
     return fail(e, VX_E_INVALID, "top-p: n %d, valid %d out of range", n, valid);
   if (!on_device) {
     std::vector<float> l(logits, logits + n);

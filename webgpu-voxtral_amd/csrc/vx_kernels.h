@@ -912,39 +912,69 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
 // generate() masking (index 0 and indices >= valid set to -inf,
 // src/engine.ts:2556-2563):
 //   s_i = f32(l_i / T); p_i = f32(exp(s_i - max)); q_i = f32(p_i / sum p)
-//   order by q descending, equal q by ascending index (a stable sort);
+//   with sum p in f64 (JS numbers), reduced in a fixed tree order;
+//   order by q descending, equal q by ascending index (the reference's
+//   stable sort);
 //   cutoff = first rank whose running sum reaches top_p;
 //   r = u * (sum of the first cutoff q); pick the first rank whose running
 //   sum reaches r.
-// Sums are in f64 as in the reference (JS numbers), reduced in a fixed tree
-// order.  u = (z >> 11) * 2^-53 for z the next output of a splitmix64
-// stream whose state lives at *rng (advanced once per call).  One block of
-// TP_NT threads; keys sorted with a bitonic network in LDS.
-constexpr int TP_NT = 1024, TP_N = 16384;  // sort width (>= n, power of 2)
+// No sort is needed.  Entry i has the unique 45-bit key
+// (0x7FFFFFFF - bits(q_i)) << 14 | i, whose ascending order is the order
+// above, and the exact mass floor(q_i * 2^62).  The running sums are exact
+// integer sums, so "the first rank whose running sum reaches t" is the
+// smallest key K with mass(keys <= K) >= t, found by a radix select (four
+// passes over 12 + 11 + 11 + 11 key bits: per-bin masses and counts by LDS
+// atomics, order-independent because they are integers; the first non-empty
+// bin whose cumulative mass reaches t).  One select gives the cutoff key
+// and its prefix mass resum; a second, with t = ceil(u * resum), gives the
+// pick.  The reference's running sums round in f64, these are exact (to
+// 2^-62 per entry): the picks differ only where a running sum lies within
+// f64 rounding of a threshold.  u = (z >> 11) * 2^-53 for z the next output
+// of a splitmix64 stream whose state lives at *rng (advanced once per
+// call).  One block of TP_NT threads.
+constexpr int TP_NT = 1024, TP_WAVES = TP_NT / 64;
+constexpr int TP_MAXN = 9216;    // largest n
+constexpr int TP_BINS = 4096;    // bins of the widest digit
+static_assert(SEMV <= TP_MAXN && TP_MAXN <= 16384 && TP_BINS == 4 * TP_NT, "top-p sizes");
+
+__device__ __forceinline__ uint64_t tp_mass(uint64_t key) {
+  const float q = __builtin_bit_cast(float, 0x7FFFFFFFu - (uint32_t)(key >> 14));
+  return (uint64_t)((double)q * 0x1p62);
+}
+
 __global__ __launch_bounds__(TP_NT) void topp_sample_kernel(const float *logits, int n, int valid,
                                                             const double *params, uint64_t *rng,
                                                             uint32_t *out) {
   const double top_p = params[0], temp = params[1];  // in device memory: graphs stay valid
-  __shared__ uint64_t key[TP_N];
-  __shared__ double part[TP_NT];
-  __shared__ double red[TP_NT / 64];
-  __shared__ int pick[2];
+  __shared__ uint64_t key[TP_MAXN];       // first holds s_i, then p_i, as floats
+  __shared__ uint64_t bmass[TP_BINS];     // also the f64 tree of the p sum
+  __shared__ uint32_t bcnt[TP_BINS];
+  __shared__ uint64_t wsum[TP_WAVES];
+  __shared__ double red[TP_WAVES];
+  __shared__ uint64_t sel_base, sel_incl, target;
+  __shared__ int sel;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  auto scaled = [&](int i) -> float {
-    return (i > 0 && i < valid && i < n) ? (float)((double)logits[i] / temp) : -INFINITY;
-  };
-  // max
+  float *sv = reinterpret_cast<float *>(key);
+  // s_i and the max
   double mx = -INFINITY;
-  for (int i = tid; i < n; i += TP_NT) mx = fmax(mx, (double)scaled(i));
+  for (int i = tid; i < n; i += TP_NT) {
+    const float si = (i > 0 && i < valid) ? (float)((double)logits[i] / temp) : -INFINITY;
+    sv[i] = si;
+    mx = fmax(mx, (double)si);
+  }
   for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
   if (lane == 0) red[wave] = mx;
   __syncthreads();
   mx = red[0];
-  for (int w = 1; w < TP_NT / 64; w++) mx = fmax(mx, red[w]);
-  __syncthreads();
-  // sum of p in f64, fixed order: per thread, then tree
+  for (int w = 1; w < TP_WAVES; w++) mx = fmax(mx, red[w]);
+  // p_i and their sum in f64: per thread, then a tree
+  double *part = reinterpret_cast<double *>(bmass);
   double s = 0.0;
-  for (int i = tid; i < n; i += TP_NT) s += (double)(float)exp((double)scaled(i) - mx);
+  for (int i = tid; i < n; i += TP_NT) {
+    const float pi = (float)exp((double)sv[i] - mx);
+    sv[i] = pi;
+    s += (double)pi;
+  }
   part[tid] = s;
   __syncthreads();
   for (int o = TP_NT / 2; o > 0; o >>= 1) {
@@ -952,91 +982,125 @@ __global__ __launch_bounds__(TP_NT) void topp_sample_kernel(const float *logits,
     __syncthreads();
   }
   const double sum = part[0];
-  __syncthreads();
-  // keys: q bits (q >= 0) high, inverted index low -> descending order is
-  // q descending, then index ascending
-  for (int i = tid; i < TP_N; i += TP_NT) {
-    uint64_t k = 0;
-    if (i < n) {
-      const float q = (float)((double)(float)exp((double)scaled(i) - mx) / sum);
-      k = ((uint64_t)__builtin_bit_cast(uint32_t, q) << 32) | (0xFFFFFFFFu - (uint32_t)i);
-    }
-    key[i] = k;
+  // keys (each thread first reads its p_i: keys overwrite the floats)
+  constexpr int PER = TP_MAXN / TP_NT;
+  float pv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = tid + j * TP_NT;
+    pv[j] = i < n ? sv[i] : 0.f;
   }
   __syncthreads();
-  for (int size = 2; size <= TP_N; size <<= 1)
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < TP_N / 2; i += TP_NT) {
-        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
-        const bool desc = (lo & size) == 0;
-        const uint64_t a = key[lo], b = key[hi];
-        if ((a < b) == desc) {
-          key[lo] = b;
-          key[hi] = a;
+#pragma unroll
+  for (int j = 0; j < PER; j++) {
+    const int i = tid + j * TP_NT;
+    if (i < n) {
+      const float q = (float)((double)pv[j] / sum);
+      key[i] = ((uint64_t)(0x7FFFFFFFu - __builtin_bit_cast(uint32_t, q)) << 14) | (uint32_t)i;
+    }
+  }
+  // smallest key K with mass(keys <= K) >= t; returns K and that mass, or
+  // found = false when the total mass stays below t
+  auto select = [&](uint64_t t, uint64_t &kout, uint64_t &incl) -> bool {
+    uint64_t prefix = 0, base = 0;
+    for (int pass = 0; pass < 4; pass++) {
+      const int width = pass == 0 ? 12 : 11, shift = 33 - 11 * pass;
+      const int hi = shift + width, nb = 1 << width;
+      for (int b = tid; b < TP_BINS; b += TP_NT) {
+        bmass[b] = 0;
+        bcnt[b] = 0;
+      }
+      if (tid == 0) sel = TP_BINS;
+      __syncthreads();
+      for (int i = tid; i < n; i += TP_NT) {
+        const uint64_t k = key[i];
+        if ((k >> hi) == prefix) {
+          const int d = (int)((k >> shift) & (uint64_t)(nb - 1));
+          atomicAdd((unsigned long long *)&bmass[d], (unsigned long long)tp_mass(k));
+          atomicAdd(&bcnt[d], 1u);
         }
       }
       __syncthreads();
-    }
-  // running sums in sorted order: each thread a contiguous run of RUN
-  constexpr int RUN = TP_N / TP_NT;
-  auto qv = [&](int r) -> double { return (double)__builtin_bit_cast(float, (uint32_t)(key[r] >> 32)); };
-  double loc = 0.0;
-  for (int j = 0; j < RUN; j++) loc += qv(tid * RUN + j);
-  part[tid] = loc;
-  __syncthreads();
-  for (int o = 1; o < TP_NT; o <<= 1) {  // inclusive scan of the run totals
-    const double v = tid >= o ? part[tid - o] : 0.0;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
-  }
-  const double base = tid ? part[tid - 1] : 0.0;
-  if (tid < 2) pick[tid] = TP_N;
-  __syncthreads();
-  {  // cutoff: first rank with running sum >= top_p
-    double c = base;
-    for (int j = 0; j < RUN; j++) {
-      c += qv(tid * RUN + j);
-      if (c >= top_p) {
-        atomicMin(&pick[0], tid * RUN + j + 1);
-        break;
+      // exclusive prefix of the mass of bins [0, 4 tid) over the block
+      uint64_t m4 = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) m4 += bmass[4 * tid + j];
+      uint64_t incw = m4;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t u = __shfl_up(incw, o, 64);
+        if (lane >= o) incw += u;
       }
+      if (lane == 63) wsum[wave] = incw;
+      __syncthreads();
+      uint64_t run = base + incw - m4;
+      for (int w = 0; w < wave; w++) run += wsum[w];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int d = 4 * tid + j;
+        if (d < nb && bcnt[d] > 0) {
+          run += bmass[d];
+          if (run >= t) {  // the running mass only grows: the smallest such d wins
+            atomicMin(&sel, d);
+            break;
+          }
+        }
+      }
+      __syncthreads();
+      const int ds = sel;
+      if (ds >= TP_BINS) return false;  // uniform: the total never reaches t
+      // the owner of bin ds publishes the mass before it and including it
+      if (tid == ds / 4) {
+        uint64_t r2 = base + incw - m4;
+        for (int w = 0; w < wave; w++) r2 += wsum[w];
+        for (int d = 4 * tid; d < ds; d++)
+          if (bcnt[d] > 0) r2 += bmass[d];
+        sel_base = r2;
+        sel_incl = r2 + bmass[ds];
+      }
+      __syncthreads();
+      base = sel_base;
+      prefix = (prefix << width) | (uint64_t)ds;
+      incl = sel_incl;
+      __syncthreads();  // bins and sel are reset by the next pass
     }
+    kout = prefix;
+    return true;
+  };
+  // cutoff: t = ceil(top_p * 2^62)
+  if (tid == 0) {
+    const double x = top_p * 0x1p62;
+    target = x <= 0.0 ? 0ull : x >= 0x1p64 ? ~0ull : (uint64_t)ceil(x);
   }
   __syncthreads();
-  const int cutoff = pick[0] < n ? pick[0] : n;
+  uint64_t kc = 0, resum = 0;  // cutoff key and the mass of keys up to it
+  if (!select(target, kc, resum)) {
+    // the cutoff is n: resum is the total mass (every entry)
+    for (int b = tid; b < TP_BINS; b += TP_NT) bmass[b] = 0;
+    __syncthreads();
+    uint64_t m = 0;
+    for (int i = tid; i < n; i += TP_NT) m += tp_mass(key[i]);
+    atomicAdd((unsigned long long *)&bmass[0], (unsigned long long)m);
+    __syncthreads();
+    resum = bmass[0];
+    __syncthreads();
+  }
+  // draw: t = ceil(u * resum) with u = u53 * 2^-53, exactly
   if (tid == 0) {
-    // resum = running sum at rank cutoff - 1, recomputed from its run
-    const int rr = cutoff - 1, t0 = rr / RUN;
-    double c = t0 ? part[t0 - 1] : 0.0;
-    for (int j = t0 * RUN; j <= rr; j++) c += qv(j);
     uint64_t z = (*rng += 0x9E3779B97F4A7C15ull);
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
     z ^= z >> 31;
-    part[0] = (double)(z >> 11) * 0x1p-53 * c;  // r (the scan is no longer needed at rank 0)
-  }
-  // part[0] is overwritten only after every thread read its base above
-  __syncthreads();
-  const double r = part[0];
-  __syncthreads();
-  {
-    double c = base;
-    for (int j = 0; j < RUN; j++) {
-      const int rank = tid * RUN + j;
-      if (rank >= cutoff) break;
-      c += qv(rank);
-      if (c >= r) {
-        atomicMin(&pick[1], rank);
-        break;
-      }
-    }
+    const uint64_t u53 = z >> 11;
+    uint64_t lo = u53 * resum, hi = __umul64hi(u53, resum);
+    const uint64_t add = (1ull << 53) - 1;
+    lo += add;
+    hi += lo < add;
+    target = (hi << 11) | (lo >> 53);
   }
   __syncthreads();
-  if (tid == 0) {
-    const int rank = pick[1] < cutoff ? pick[1] : 0;
-    *out = 0xFFFFFFFFu - (uint32_t)(key[rank] & 0xFFFFFFFFu);
-  }
+  uint64_t kp = 0, dummy = 0;
+  if (!select(target, kp, dummy)) select(0, kp, dummy);  // (t <= resum: not reached)
+  if (tid == 0) *out = (uint32_t)(kp & 0x3FFF);
 }
 
 // ------------------------------------------------------------- FM kernels
