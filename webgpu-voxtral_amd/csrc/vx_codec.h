@@ -2,9 +2,9 @@
 // waveform) on MFMA: codecDecode, src/engine.ts:1402-1713, with the codec
 // shaders of src/shaders.ts:817-1110, 1432-1868.
 //
-// Every projection and convolution is a GEMM on v_mfma_f32_16x16x32_f16
-// (pf_gemm_kernel): the f16 weights are the A operand and the activations
-// the packed hi/lo B operand, so products keep f32 accuracy.
+// Every projection and convolution is one f16 x f16 -> f32 GEMM on the
+// matrix cores (hipBLASLt, vx_blas.h): the f16 weights times the
+// activations in hi/lo f16 form, so products keep f32 accuracy.
 //   - the causal convs become GEMMs over an im2col B (k-major: column t holds
 //     x[t - (k_size-1) + kk][ci] at k = kk * c_in + ci) with the weights
 //     reordered to match once after loading; their weight norm g/||w|| is
@@ -16,7 +16,8 @@
 //   - the input conv's B is gathered straight from the codes (vqLookup,
 //     fsqDequant and concatCodecInput fused into the packing).
 // Tokens are processed in column chunks of at most CX_MAXT; a chunk's B
-// holds nc = 2 * nt columns (nt = tokens rounded up to 128, hi then lo).
+// holds nc = 2 * nt columns (nt = tokens rounded up to 128, hi then lo),
+// each column's K halves contiguous; the GEMM output C is [nc][M].
 #pragma once
 #include "vx_prefill.h"
 
@@ -34,30 +35,25 @@ constexpr int CX_STAGES = 4, CX_LPS = 2;
 constexpr int CX_FRAME_SAMPLES = 8 * CPATCH;  // 1920 samples = 80 ms at 24 kHz
 constexpr int CX_MAXT = 1024;                 // tokens per GEMM chunk
 constexpr int CX_NC = 2 * CX_MAXT;
-constexpr size_t CX_CCAP = (size_t)CX_NC * 2 * CHID;  // GEMM output floats (all split slabs)
+constexpr size_t CX_CCAP = (size_t)CX_NC * 2 * CHID;  // GEMM output floats
 constexpr float CX_NORM_EPS = 0.01f, CX_QK_EPS = 1e-6f;
 static_assert(CKIN % 32 == 0 && CKIN >= CIN * CK_IN, "input conv k padding");
 
-// output (token t, row m) of a chunk's GEMM: hi and lo columns of the S
-// split slabs, summed in a fixed order
-__device__ __forceinline__ float cx_val(const float *C, int ldc, int nc, int S, int t, int m) {
-  const int nt = nc >> 1;
-  float y = 0.f;
-  for (int s = 0; s < S; s++, C += (size_t)nc * ldc)
-    y += C[(size_t)t * ldc + m] + C[(size_t)(nt + t) * ldc + m];
-  return y;
+// output (token t, row m) of a chunk's GEMM: hi column plus lo column
+__device__ __forceinline__ float cx_val(const float *C, int ldc, int nc, int t, int m) {
+  return C[(size_t)t * ldc + m] + C[(size_t)((nc >> 1) + t) * ldc + m];
 }
 
-// columns t (hi) and nt + t (lo) of k group kb
-__device__ __forceinline__ void cx_put(h8 *B, int nc, int kb, int t, const float (&y)[8]) {
+// k group kb (8 halves) of columns t (hi) and nt + t (lo); kg = K / 8
+__device__ __forceinline__ void cx_put(h8 *B, int nc, int kg, int kb, int t, const float (&y)[8]) {
   h8 hi, lo;
 #pragma unroll
   for (int e = 0; e < 8; e++) {
     hi[e] = (_Float16)y[e];
     lo[e] = (_Float16)(y[e] - (float)hi[e]);
   }
-  B[(size_t)kb * nc + t] = hi;
-  B[(size_t)kb * nc + (nc >> 1) + t] = lo;
+  B[(size_t)t * kg + kb] = hi;
+  B[(size_t)((nc >> 1) + t) * kg + kb] = lo;
 }
 
 // ------------------------------------------------------------- packing
@@ -86,7 +82,7 @@ __global__ __launch_bounds__(256) void cx_pack_kernel(const float *X, int K, int
       const int k = kb * 8 + e;
       y[e] = live ? (NORM ? x[k] * r * h2f(g[k]) : x[k]) : 0.f;
     }
-    cx_put(B, nc, kb, t, y);
+    cx_put(B, nc, K / 8, kb, t, y);
   }
 }
 
@@ -118,7 +114,7 @@ __global__ __launch_bounds__(128) void cx_pack_in_kernel(const uint16_t *cbn, co
       const int src = tau - (CK_IN - 1) + kk;
       y[e] = (t < n && k < CIN * CK_IN && src >= 0) ? cx_feature(cbn, sem, ac, levels, src, ci) : 0.f;
     }
-    cx_put(B, nc, kb, t, y);
+    cx_put(B, nc, CKIN / 8, kb, t, y);
   }
 }
 
@@ -133,7 +129,7 @@ __global__ __launch_bounds__(256) void cx_pack_up_kernel(const float *X, const f
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) y[e] = ok ? scale[ci0 + e] * X[(size_t)src * CD + ci0 + e] : 0.f;
-    cx_put(B, nc, kb, t, y);
+    cx_put(B, nc, CKUP / 8, kb, t, y);
   }
 }
 
@@ -148,46 +144,46 @@ __global__ __launch_bounds__(256) void cx_pack_out_kernel(const float *X, int t0
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) y[e] = ok ? X[(size_t)src * CD + ci0 + e] : 0.f;
-    cx_put(B, nc, kb, t, y);
+    cx_put(B, nc, CKOUT / 8, kb, t, y);
   }
 }
 
 // ----------------------------------------------------------- epilogues
 // out[(t0 + t) * ldo + m] = rs[m] * y (conv weight norm g / ||w|| per
 // output channel), m < mv.  Grid: (n, ceil(mv / 256)).
-__global__ void cx_scale_rows_epi_kernel(const float *C, int ldc, int nc, int S, int t0,
-                                         const float *rs, int mv, float *out, int ldo) {
+__global__ void cx_scale_rows_epi_kernel(const float *C, int ldc, int nc, int t0, const float *rs,
+                                         int mv, float *out, int ldo) {
   const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
-  if (m < mv) out[(size_t)(t0 + t) * ldo + m] = rs[m] * cx_val(C, ldc, nc, S, t, m);
+  if (m < mv) out[(size_t)(t0 + t) * ldo + m] = rs[m] * cx_val(C, ldc, nc, t, m);
 }
 
 // transposed conv output: step 2 (t0 + t) + r, channel co from row r * CD + co.
 // Grid: (n, 2 * CD / 256).
-__global__ void cx_up_epi_kernel(const float *C, int nc, int S, int t0, float *out) {
+__global__ void cx_up_epi_kernel(const float *C, int nc, int t0, float *out) {
   const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
   const int r = m / CD, co = m - r * CD;
-  out[(size_t)(2 * (t0 + t) + r) * CD + co] = cx_val(C, 2 * CD, nc, S, t, m);
+  out[(size_t)(2 * (t0 + t) + r) * CD + co] = cx_val(C, 2 * CD, nc, t, m);
 }
 
 // layer scale + residual (batchedLayerScale, src/shaders.ts:1755-1781):
 // X = y * scale + X.  Grid: (n, CD / 256).
-__global__ void cx_resid_epi_kernel(const float *C, int nc, int S, int t0, const uint16_t *scale,
+__global__ void cx_resid_epi_kernel(const float *C, int nc, int t0, const uint16_t *scale,
                                     float *X) {
   const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
   float *x = X + (size_t)(t0 + t) * CD + m;
-  *x = cx_val(C, CD, nc, S, t, m) * h2f(scale[m]) + *x;
+  *x = cx_val(C, CD, nc, t, m) * h2f(scale[m]) + *x;
 }
 
 // q, k, v from the stacked projection, q and k RMS-normalised per head
 // (qkNorm, src/shaders.ts:1787-1830: weight [CNH * CHDIM] read at h * CHDIM).
 // One wave per (token, part, head); grid (n, 3 * CNH / 4) of 256.
-__global__ __launch_bounds__(256) void cx_qkv_epi_kernel(const float *C, int nc, int S, int t0,
+__global__ __launch_bounds__(256) void cx_qkv_epi_kernel(const float *C, int nc, int t0,
                                                          const uint16_t *qn, const uint16_t *kn,
                                                          float *Q, float *K, float *V) {
   const int t = blockIdx.x, gi = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int part = gi / CNH, h = gi - part * CNH, d = 2 * lane;
   const int m = part * CD + h * CHDIM + d;
-  float y0 = cx_val(C, 3 * CD, nc, S, t, m), y1 = cx_val(C, 3 * CD, nc, S, t, m + 1);
+  float y0 = cx_val(C, 3 * CD, nc, t, m), y1 = cx_val(C, 3 * CD, nc, t, m + 1);
   if (part < 2) {
     const float ss = wave_sum(y0 * y0 + y1 * y1);
     const float r = 1.0f / sqrtf(ss / (float)CHDIM + CX_QK_EPS);
@@ -202,8 +198,7 @@ __global__ __launch_bounds__(256) void cx_qkv_epi_kernel(const float *C, int nc,
 // SwiGLU of the stacked gate/up projection (batchedSwiGLU,
 // src/shaders.ts:1697-1716), written as the packed B of the down projection
 // (k = hidden unit).  Grid: (nt, CHID / 8 / 256) of 256; columns t >= n are 0.
-__global__ __launch_bounds__(256) void cx_swiglu_epi_kernel(const float *C, int nc, int S, int n,
-                                                            h8 *B) {
+__global__ __launch_bounds__(256) void cx_swiglu_epi_kernel(const float *C, int nc, int n, h8 *B) {
   const int t = blockIdx.x, kb = blockIdx.y * 256 + threadIdx.x;
   float y[8];
 #pragma unroll
@@ -211,12 +206,12 @@ __global__ __launch_bounds__(256) void cx_swiglu_epi_kernel(const float *C, int 
     float a = 0.f;
     if (t < n) {
       const int m = kb * 8 + e;
-      const float g = cx_val(C, 2 * CHID, nc, S, t, m), u = cx_val(C, 2 * CHID, nc, S, t, CHID + m);
+      const float g = cx_val(C, 2 * CHID, nc, t, m), u = cx_val(C, 2 * CHID, nc, t, CHID + m);
       a = g / (1.0f + expf(-g)) * u;
     }
     y[e] = a;
   }
-  cx_put(B, nc, kb, t, y);
+  cx_put(B, nc, CHID / 8, kb, t, y);
 }
 
 // ----------------------------------------------------------- attention

@@ -20,6 +20,7 @@
 #include "vx_kernels.h"
 #include "vx_prefill.h"
 #include "vx_codec.h"
+#include "vx_blas.h"
 #include "vx_loader.h"
 #include "vx_tokenizer.h"
 
@@ -145,6 +146,11 @@ struct vx_engine {
   h8 *cx_b = nullptr;
   uint32_t *cx_sem = nullptr, *cx_ac = nullptr;
   int cx_chunk = CX_MAXT;  // tokens per codec GEMM chunk (multiple of 128)
+
+  // the plain GEMMs of the prefill and the codec (hipBLASLt), set up on
+  // first use
+  BlasGemm blas;
+  bool blas_ready = false;
 
   void weights_changed() {
     tproj_ready = false;
@@ -1339,16 +1345,24 @@ int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos) {
 // rows are already on the device.  Afterwards the residual stream and
 // W.normed hold the last token's values and the position is advanced, as
 // after n single steps.
-// k splits of the narrow prefill GEMMs (grid >= 192 blocks; the split
-// slabs fit the GEMM output buffer of the stacked gate/up GEMM)
-constexpr int PF_S_QKV = 3, PF_S_O = 4, PF_S_DOWN = 6;
-static_assert(PF_S_QKV * QKV_ROWS <= 2 * HID && PF_S_O * DIM <= 2 * HID &&
-                  PF_S_DOWN * DIM <= 2 * HID && (DIM / 32) % PF_S_QKV == 0 &&
-                  (QD / 32) % PF_S_O == 0 && (HID / 32) % PF_S_DOWN == 0,
-              "prefill k splits");
+static int blas_setup(vx_engine *e) {
+  if (e->blas_ready) return VX_OK;
+  const std::string err = e->blas.init(size_t(64) << 20);
+  if (!err.empty()) return fail(e, VX_E_DEVICE, "%s", err.c_str());
+  e->blas_ready = true;
+  return VX_OK;
+}
 
-static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int vcount,
-                                  bool has_voice) {
+// C[n][m] = sum_k W[m][k] B[n][k] on the engine's stream
+static int blas_gemm(vx_engine *e, const uint16_t *W, int M, int K, const h8 *B, int N, float *C) {
+  const std::string err = e->blas.gemm(W, M, K, (const uint16_t *)B, N, C, e->st);
+  if (!err.empty()) return fail(e, VX_E_DEVICE, "%s (M %d, K %d, N %d)", err.c_str(), M, K, N);
+  return VX_OK;
+}
+
+static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int vcount,
+                                 bool has_voice) {
+  int rc = VX_OK;
   hipStream_t st = e->st;
   const int pos0 = e->host_pos;
   hipLaunchKernelGGL(pf_embed_kernel, dim3(n, DIM / 256), dim3(256), 0, st, e->tok_emb, e->pf_tok,
@@ -1358,11 +1372,9 @@ static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int
     const LayerW &W = e->L[l];
     hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
                        W.attn_norm, e->cfg.norm_eps, e->pf_b);
-    hipLaunchKernelGGL(pf_gemm_kernel<DIM>, dim3(QKV_ROWS / PF_BM, PF_NC / PF_BN, PF_S_QKV), blk, 0,
-                       st, W.wqkv, e->pf_b, e->pf_c, QKV_ROWS, PF_NC);
+    if ((rc = blas_gemm(e, W.wqkv, QKV_ROWS, DIM, e->pf_b, PF_NC, e->pf_c))) return rc;
     hipLaunchKernelGGL(pf_qkv_epi_kernel, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c,
-                       PF_S_QKV, e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0,
-                       e->inv_freq);
+                       e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
     if (e->kv_f32)
       hipLaunchKernelGGL(pf_attn_kernel<float>, dim3(n, NKV), blk, 0, st, e->pf_q, e->kc(l),
                          e->vc(l), e->max_seq, pos0, e->pf_attn);
@@ -1371,28 +1383,24 @@ static void enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int
                          e->vc(l), e->max_seq, pos0, e->pf_attn);
     hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_attn, QD, n,
                        nullptr, 0.f, e->pf_b);
-    hipLaunchKernelGGL(pf_gemm_kernel<QD>, dim3(DIM / PF_BM, PF_NC / PF_BN, PF_S_O), blk, 0, st,
-                       W.wo, e->pf_b, e->pf_c, DIM, PF_NC);
-    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, PF_S_O,
-                       e->pf_x);
+    if ((rc = blas_gemm(e, W.wo, DIM, QD, e->pf_b, PF_NC, e->pf_c))) return rc;
+    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, e->pf_x);
     hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
                        W.ffn_norm, e->cfg.norm_eps, e->pf_b);
     // W1 and W3 are adjacent in the arena: one GEMM over the stacked rows
-    hipLaunchKernelGGL(pf_gemm_kernel<DIM>, dim3(2 * HID / PF_BM, PF_NC / PF_BN), blk, 0, st, W.w1,
-                       e->pf_b, e->pf_c, 2 * HID, PF_NC);
+    if ((rc = blas_gemm(e, W.w1, 2 * HID, DIM, e->pf_b, PF_NC, e->pf_c))) return rc;
     hipLaunchKernelGGL(pf_swiglu_epi_kernel, dim3(n, HID / 256), blk, 0, st, e->pf_c, e->pf_act);
     hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_act, HID, n,
                        nullptr, 0.f, e->pf_b);
-    hipLaunchKernelGGL(pf_gemm_kernel<HID>, dim3(DIM / PF_BM, PF_NC / PF_BN, PF_S_DOWN), blk, 0, st,
-                       W.w2, e->pf_b, e->pf_c, DIM, PF_NC);
-    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM,
-                       PF_S_DOWN, e->pf_x);
+    if ((rc = blas_gemm(e, W.w2, DIM, HID, e->pf_b, PF_NC, e->pf_c))) return rc;
+    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, e->pf_x);
   }
   (void)hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * DIM, DIM * 4, hipMemcpyDeviceToDevice, st);
   hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, e->x, e->final_norm,
                      e->cfg.norm_eps, e->normed, nullptr);
   hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, st, e->pos, pos0 + n);
   e->host_pos = pos0 + n;
+  return VX_OK;
 }
 
 int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t audio_start,
@@ -1409,6 +1417,7 @@ int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t au
       return fail(e, VX_E_INVALID, "token %d out of range", tokens[i]);
   if (e->L[0].w3 != e->L[0].w1 + (size_t)HID * DIM)
     return fail(e, VX_E_STATE, "weight layout: gate and up matrices not adjacent");
+  if ((rc = blas_setup(e))) return rc;
   const bool has_voice = voice && audio_count > 0;
   for (int c0 = 0; c0 < n_tokens; c0 += PF_MAXT) {
     const int n = std::min(PF_MAXT, n_tokens - c0);
@@ -1424,7 +1433,7 @@ int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t au
         vc = b - a;
       }
     }
-    enqueue_prefill_chunk(e, n, c0, vs, vc, vc > 0);
+    if ((rc = enqueue_prefill_chunk(e, n, c0, vs, vc, vc > 0))) return rc;
     LAUNCHCHK(e);
     HIPCHK(e, hipStreamSynchronize(e->st));  // the host buffers above are reused per chunk
   }
@@ -1573,32 +1582,6 @@ static int codec_reserve(vx_engine *e, int T) {
   return VX_OK;
 }
 
-// C[S][nc][M] = A[M][K] x B[K][nc] with a k split S that fills the chip
-// (>= 256 blocks) while the slabs fit the output buffer; returns S
-extern "C++" {
-template <int K>
-static int cx_gemm_k(vx_engine *e, const uint16_t *A, int M, int nc) {
-  const int blocks = (M / PF_BM) * (nc / PF_BN);
-  int S = 1;
-  while (S < 8 && blocks * S < 256 && (K / 32) % (2 * S) == 0 &&
-         (size_t)2 * S * nc * M <= CX_CCAP)
-    S *= 2;
-  hipLaunchKernelGGL(pf_gemm_kernel<K>, dim3(M / PF_BM, nc / PF_BN, S), dim3(256), 0, e->st, A,
-                     e->cx_b, e->cx_c, M, nc);
-  return S;
-}
-}  // extern "C++"
-
-static int cx_gemm(vx_engine *e, int K, const uint16_t *A, int M, int nc) {
-  switch (K) {
-    case CKIN: return cx_gemm_k<CKIN>(e, A, M, nc);
-    case CD: return cx_gemm_k<CD>(e, A, M, nc);
-    case CKUP: return cx_gemm_k<CKUP>(e, A, M, nc);
-    case CHID: return cx_gemm_k<CHID>(e, A, M, nc);
-    default: return cx_gemm_k<CKOUT>(e, A, M, nc);
-  }
-}
-
 // the intermediates of debugCodecDecode (src/engine.ts:1719-1985)
 static int cx_stop_frames(int T, int stop) {
   if (stop <= VX_CODEC_STOP_STAGE0) return T;
@@ -1611,6 +1594,7 @@ static int cx_stop_frames(int T, int stop) {
 // leaves the result in *res (device) with *count floats
 static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *count) {
   hipStream_t st = e->st;
+  int rc = VX_OK;  // the first GEMM failure; later launches only queue work
   const CodecW &w = e->cw;
   const int levels = e->cfg.acoustic_levels;
   const dim3 blk(256);
@@ -1632,9 +1616,9 @@ static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *c
   chunks(T, [&](int t0, int n, int nc) {
     hipLaunchKernelGGL(cx_pack_in_kernel, dim3(nc / 2), dim3(128), 0, st, e->cx_cb, e->cx_sem,
                        e->cx_ac, levels, t0, n, nc, e->cx_b);
-    const int S = cx_gemm(e, CKIN, e->cx_ain, CD, nc);
-    hipLaunchKernelGGL(cx_scale_rows_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, CD, nc, S,
-                       t0, e->cx_rs_in, CD, e->cx_x, CD);
+    if (!rc) rc = blas_gemm(e, e->cx_ain, CD, CKIN, e->cx_b, nc, e->cx_c);
+    hipLaunchKernelGGL(cx_scale_rows_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, CD, nc, t0,
+                       e->cx_rs_in, CD, e->cx_x, CD);
   });
   int TT = T, at = VX_CODEC_STOP_INPUT_CONV;
   float *x = e->cx_x, *x2 = e->cx_x2;
@@ -1645,8 +1629,8 @@ static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *c
       chunks(TT, [&](int t0, int n, int nc) {
         hipLaunchKernelGGL(cx_pack_kernel<true>, dim3(nc / 2), blk, 0, st, x, CD, t0, n, nc,
                            L.attn_norm, CX_NORM_EPS, e->cx_b);
-        const int S = cx_gemm(e, CD, L.wqkv, 3 * CD, nc);
-        hipLaunchKernelGGL(cx_qkv_epi_kernel, dim3(n, 3 * CNH / 4), blk, 0, st, e->cx_c, nc, S, t0,
+        if (!rc) rc = blas_gemm(e, L.wqkv, 3 * CD, CD, e->cx_b, nc, e->cx_c);
+        hipLaunchKernelGGL(cx_qkv_epi_kernel, dim3(n, 3 * CNH / 4), blk, 0, st, e->cx_c, nc, t0,
                            L.q_norm, L.k_norm, e->cx_q, e->cx_k, e->cx_v);
       });
       hipLaunchKernelGGL(cx_attn_kernel, dim3(TT, CNH / 4), blk, 0, st, e->cx_q, e->cx_k, e->cx_v,
@@ -1654,19 +1638,19 @@ static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *c
       chunks(TT, [&](int t0, int n, int nc) {
         hipLaunchKernelGGL(cx_pack_kernel<false>, dim3(nc / 2), blk, 0, st, e->cx_attn, CD, t0, n,
                            nc, nullptr, 0.f, e->cx_b);
-        const int S = cx_gemm(e, CD, L.wo, CD, nc);
-        hipLaunchKernelGGL(cx_resid_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, S, t0,
+        if (!rc) rc = blas_gemm(e, L.wo, CD, CD, e->cx_b, nc, e->cx_c);
+        hipLaunchKernelGGL(cx_resid_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, t0,
                            L.attn_scale, x);
       });
       chunks(TT, [&](int t0, int n, int nc) {
         hipLaunchKernelGGL(cx_pack_kernel<true>, dim3(nc / 2), blk, 0, st, x, CD, t0, n, nc,
                            L.ffn_norm, CX_NORM_EPS, e->cx_b);
-        int S = cx_gemm(e, CD, L.w13, 2 * CHID, nc);
+        if (!rc) rc = blas_gemm(e, L.w13, 2 * CHID, CD, e->cx_b, nc, e->cx_c);
         // the gate/up GEMM has consumed B: the SwiGLU epilogue refills it
         hipLaunchKernelGGL(cx_swiglu_epi_kernel, dim3(nc / 2, CHID / 8 / 256), blk, 0, st, e->cx_c,
-                           nc, S, n, e->cx_b);
-        S = cx_gemm(e, CHID, L.w2, CD, nc);
-        hipLaunchKernelGGL(cx_resid_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, S, t0,
+                           nc, n, e->cx_b);
+        if (!rc) rc = blas_gemm(e, L.w2, CD, CHID, e->cx_b, nc, e->cx_c);
+        hipLaunchKernelGGL(cx_resid_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, t0,
                            L.ffn_scale, x);
       });
     }
@@ -1676,13 +1660,14 @@ static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *c
     chunks(TT, [&](int t0, int n, int nc) {
       hipLaunchKernelGGL(cx_pack_up_kernel, dim3(nc / 2), blk, 0, st, x, e->cx_s_up[s], t0, n, nc,
                          e->cx_b);
-      const int S = cx_gemm(e, CKUP, e->cx_aup[s], 2 * CD, nc);
-      hipLaunchKernelGGL(cx_up_epi_kernel, dim3(n, 2 * CD / 256), blk, 0, st, e->cx_c, nc, S, t0, x2);
+      if (!rc) rc = blas_gemm(e, e->cx_aup[s], 2 * CD, CKUP, e->cx_b, nc, e->cx_c);
+      hipLaunchKernelGGL(cx_up_epi_kernel, dim3(n, 2 * CD / 256), blk, 0, st, e->cx_c, nc, t0, x2);
     });
     std::swap(x, x2);
     TT *= 2;
     at = VX_CODEC_STOP_STAGE0 + 2 * s + 1;
   }
+  if (rc) return rc;
   if (stop != VX_CODEC_STOP_AUDIO) {
     *res = x;
     *count = (size_t)TT * CD;
@@ -1692,10 +1677,11 @@ static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *c
   // [240 t, 240 t + 240)
   chunks(TT, [&](int t0, int n, int nc) {
     hipLaunchKernelGGL(cx_pack_out_kernel, dim3(nc / 2), blk, 0, st, x, t0, n, nc, e->cx_b);
-    const int S = cx_gemm(e, CKOUT, e->cx_aout, CPATCH_ROWS, nc);
+    if (!rc) rc = blas_gemm(e, e->cx_aout, CPATCH_ROWS, CKOUT, e->cx_b, nc, e->cx_c);
     hipLaunchKernelGGL(cx_scale_rows_epi_kernel, dim3(n, 1), blk, 0, st, e->cx_c, CPATCH_ROWS, nc,
-                       S, t0, e->cx_rs_out, CPATCH, e->cx_audio, CPATCH);
+                       t0, e->cx_rs_out, CPATCH, e->cx_audio, CPATCH);
   });
+  if (rc) return rc;
   *res = e->cx_audio;
   *count = (size_t)TT * CPATCH;
   return VX_OK;
@@ -1713,7 +1699,8 @@ static int codec_decode_impl(vx_engine *e, const uint32_t *semantic, const uint3
   if (out_count < vx_codec_stop_count(n_frames, stop))
     return fail(e, VX_E_INVALID, "output holds %zu floats, %zu needed", out_count,
                 vx_codec_stop_count(n_frames, stop));
-  if ((rc = codec_prepare(e)) || (rc = codec_reserve(e, n_frames))) return rc;
+  if ((rc = codec_prepare(e)) || (rc = codec_reserve(e, n_frames)) || (rc = blas_setup(e)))
+    return rc;
   HIPCHK(e, hipMemcpyAsync(e->cx_sem, semantic, (size_t)n_frames * 4, hipMemcpyHostToDevice, e->st));
   HIPCHK(e, hipMemcpyAsync(e->cx_ac, acoustic, (size_t)n_frames * NAC * 4, hipMemcpyHostToDevice,
                            e->st));
