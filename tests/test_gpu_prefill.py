@@ -3,6 +3,8 @@ against the reference semantics, one backboneStep per prompt token
 (src/engine.ts:2457-2472), as restated by the oracle: the KV cache of every
 layer, the last token's W.normed and the position afterwards, with voice
 rows spliced over [audio_start, audio_start + audio_count)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -31,11 +33,13 @@ def check_kv(g, o, layers, npos, bar=1e-3):
             assert err < bar, (l, w, err)
 
 
-@pytest.mark.parametrize("n,a_start,a_count", [(40, 5, 8), (7, 0, 0), (256, 2, 64)])
-def test_prefill_matches_single_steps(n, a_start, a_count):
-    print(f"[prefill] 2 layers, {n} tokens, voice rows {a_start}+{a_count}", flush=True)
-    g = gpu_engine(n_layers=2, max_seq=512)
-    o = oracle_engine(n_layers=2, max_seq=512)
+@pytest.mark.parametrize("n,a_start,a_count,layers", [(40, 5, 8, 2), (7, 0, 0, 2), (256, 2, 64, 2),
+                                                    (520, 100, 218, 1)])
+def test_prefill_matches_single_steps(n, a_start, a_count, layers):
+    """One chunk: GEMM columns sized to the prompt (2 x n rounded up to 128)."""
+    print(f"[prefill] {layers} layers, {n} tokens, voice rows {a_start}+{a_count}", flush=True)
+    g = gpu_engine(n_layers=layers, max_seq=1024)
+    o = oracle_engine(n_layers=layers, max_seq=1024)
     try:
         rng = np.random.default_rng(n)
         tokens = rng.integers(0, 131072, n)
@@ -43,7 +47,7 @@ def test_prefill_matches_single_steps(n, a_start, a_count):
         g.prefill(tokens, a_start, a_count, voice if a_count else None)
         oracle_prefill(o, tokens, a_start, a_count, voice if a_count else None)
         assert g.position == n
-        check_kv(g, o, 2, n)
+        check_kv(g, o, layers, n)
         assert max_rel_err(g.debug_read("normed", 3072), o.buffer("normed")) < 1e-3
         # decoding continues from the prefilled state
         _, gn = g.backbone_step(24, 1)
@@ -55,10 +59,14 @@ def test_prefill_matches_single_steps(n, a_start, a_count):
 
 
 def test_prefill_two_chunks_after_context():
-    """300 tokens on top of 10 cached positions: chunks of 256 and 44, the
-    second attending to the first through the cache."""
-    print("[prefill] 1 layer, 10 + 300 tokens", flush=True)
-    g = gpu_engine(n_layers=1, max_seq=512)
+    """300 tokens on top of 10 cached positions in 256-token chunks: chunks
+    of 256 and 44, the second attending to the first through the cache."""
+    print("[prefill] 1 layer, 10 + 300 tokens, 256-token chunks", flush=True)
+    os.environ["VX_PREFILL_CHUNK"] = "256"
+    try:
+        g = gpu_engine(n_layers=1, max_seq=512)
+    finally:
+        del os.environ["VX_PREFILL_CHUNK"]
     o = oracle_engine(n_layers=1, max_seq=512)
     try:
         rng = np.random.default_rng(7)

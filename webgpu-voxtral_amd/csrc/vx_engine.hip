@@ -116,6 +116,7 @@ struct vx_engine {
         *pf_voice = nullptr;
   h8 *pf_b = nullptr;
   int32_t *pf_tok = nullptr;
+  int pf_chunk = PF_MAXT;  // tokens per prefill chunk (multiple of 128)
 
   int host_pos = 0;
   hipGraphExec_t step_exec = nullptr, hold_exec = nullptr, frame_exec = nullptr,
@@ -780,13 +781,17 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
       *q.first = p;
       p += align256(q.second);
     }
-    if (const char *ch = getenv("VX_CODEC_CHUNK")) {  // tokens per codec GEMM (tuning, tests)
+    if (const char *ch = getenv("VX_CODEC_CHUNK")) {  // (codec engines only)  // tokens per codec GEMM (tuning, tests)
       const int v = atoi(ch);
       if (v >= 128 && v <= CX_MAXT && v % 128 == 0) e->cx_chunk = v;
     }
   }
 
   // ---- batched prefill buffers (one chunk of PF_MAXT tokens)
+  if (const char *ch = getenv("VX_PREFILL_CHUNK")) {  // tokens per prefill chunk (tuning, tests)
+    const int v = atoi(ch);
+    if (v >= 128 && v <= PF_MAXT && v % 128 == 0) e->pf_chunk = v;
+  }
   {
     std::vector<std::pair<void **, size_t>> parts = {
         {(void **)&e->pf_x, (size_t)PF_MAXT * DIM * 4},
@@ -1363,6 +1368,7 @@ static int blas_gemm(vx_engine *e, const uint16_t *W, int M, int K, const h8 *B,
 static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int vcount,
                                  bool has_voice) {
   int rc = VX_OK;
+  const int nt = pf_nt(n), N = 2 * nt;
   hipStream_t st = e->st;
   const int pos0 = e->host_pos;
   hipLaunchKernelGGL(pf_embed_kernel, dim3(n, DIM / 256), dim3(256), 0, st, e->tok_emb, e->pf_tok,
@@ -1370,10 +1376,10 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
   const dim3 blk(256);
   for (int l = 0; l < e->cfg.n_layers; l++) {
     const LayerW &W = e->L[l];
-    hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
+    hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(nt), blk, 0, st, e->pf_x, DIM, n, nt,
                        W.attn_norm, e->cfg.norm_eps, e->pf_b);
-    if ((rc = blas_gemm(e, W.wqkv, QKV_ROWS, DIM, e->pf_b, PF_NC, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_qkv_epi_kernel, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c,
+    if ((rc = blas_gemm(e, W.wqkv, QKV_ROWS, DIM, e->pf_b, N, e->pf_c))) return rc;
+    hipLaunchKernelGGL(pf_qkv_epi_kernel, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c, nt,
                        e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
     if (e->kv_f32)
       hipLaunchKernelGGL(pf_attn_kernel<float>, dim3(n, NKV), blk, 0, st, e->pf_q, e->kc(l),
@@ -1381,19 +1387,22 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
     else
       hipLaunchKernelGGL(pf_attn_kernel<uint16_t>, dim3(n, NKV), blk, 0, st, e->pf_q, e->kc(l),
                          e->vc(l), e->max_seq, pos0, e->pf_attn);
-    hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_attn, QD, n,
+    hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(nt), blk, 0, st, e->pf_attn, QD, n, nt,
                        nullptr, 0.f, e->pf_b);
-    if ((rc = blas_gemm(e, W.wo, DIM, QD, e->pf_b, PF_NC, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, e->pf_x);
-    hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(PF_MAXT), blk, 0, st, e->pf_x, DIM, n,
+    if ((rc = blas_gemm(e, W.wo, DIM, QD, e->pf_b, N, e->pf_c))) return rc;
+    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, nt,
+                       e->pf_x);
+    hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(nt), blk, 0, st, e->pf_x, DIM, n, nt,
                        W.ffn_norm, e->cfg.norm_eps, e->pf_b);
     // W1 and W3 are adjacent in the arena: one GEMM over the stacked rows
-    if ((rc = blas_gemm(e, W.w1, 2 * HID, DIM, e->pf_b, PF_NC, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_swiglu_epi_kernel, dim3(n, HID / 256), blk, 0, st, e->pf_c, e->pf_act);
-    hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(PF_MAXT), blk, 0, st, e->pf_act, HID, n,
+    if ((rc = blas_gemm(e, W.w1, 2 * HID, DIM, e->pf_b, N, e->pf_c))) return rc;
+    hipLaunchKernelGGL(pf_swiglu_epi_kernel, dim3(n, HID / 256), blk, 0, st, e->pf_c, nt,
+                       e->pf_act);
+    hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(nt), blk, 0, st, e->pf_act, HID, n, nt,
                        nullptr, 0.f, e->pf_b);
-    if ((rc = blas_gemm(e, W.w2, DIM, HID, e->pf_b, PF_NC, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, e->pf_x);
+    if ((rc = blas_gemm(e, W.w2, DIM, HID, e->pf_b, N, e->pf_c))) return rc;
+    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, nt,
+                       e->pf_x);
   }
   (void)hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * DIM, DIM * 4, hipMemcpyDeviceToDevice, st);
   hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, e->x, e->final_norm,
@@ -1419,8 +1428,8 @@ int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t au
     return fail(e, VX_E_STATE, "weight layout: gate and up matrices not adjacent");
   if ((rc = blas_setup(e))) return rc;
   const bool has_voice = voice && audio_count > 0;
-  for (int c0 = 0; c0 < n_tokens; c0 += PF_MAXT) {
-    const int n = std::min(PF_MAXT, n_tokens - c0);
+  for (int c0 = 0; c0 < n_tokens; c0 += e->pf_chunk) {
+    const int n = std::min(e->pf_chunk, n_tokens - c0);
     HIPCHK(e, hipMemcpyAsync(e->pf_tok, tokens + c0, (size_t)n * 4, hipMemcpyHostToDevice, e->st));
     // voice rows of this chunk, at chunk-local offsets
     int vs = 0, vc = 0;

@@ -16,12 +16,15 @@
 
 namespace vx {
 
-constexpr int PF_MAXT = 256;           // tokens per chunk
-constexpr int PF_NC = 2 * PF_MAXT;     // B columns (hi, lo)
+constexpr int PF_MAXT = 1024;          // tokens per chunk, at most
+constexpr int PF_NC = 2 * PF_MAXT;     // B columns (hi, lo), at most
+// A chunk of n tokens uses nt = n rounded up to 128 hi columns and as many
+// lo columns: N = 2 nt GEMM columns.
+__host__ __device__ constexpr int pf_nt(int n) { return (n + 127) / 128 * 128; }
 
 // value of output (token t, row m): hi column plus lo column
-__device__ __forceinline__ float pf_c(const float *C, int ldc, int t, int m) {
-  return C[(size_t)t * ldc + m] + C[(size_t)(PF_MAXT + t) * ldc + m];
+__device__ __forceinline__ float pf_c(const float *C, int ldc, int nt, int t, int m) {
+  return C[(size_t)t * ldc + m] + C[(size_t)(nt + t) * ldc + m];
 }
 
 // ------------------------------------------------------- per-token kernels
@@ -39,11 +42,11 @@ __global__ void pf_embed_kernel(const uint16_t *table, const int32_t *tokens, co
   X[(size_t)t * DIM + i] = v;
 }
 
-// B columns t and PF_MAXT + t (K halves each) from row t of X, optionally
+// B columns t and nt + t (K halves each) from row t of X, optionally
 // RMS-normalised with gains g (rmsNorm, src/shaders.ts:137-183); columns of
-// tokens t >= n are zero.  Grid: PF_MAXT blocks of 256.
+// tokens t >= n are zero.  Grid: nt blocks of 256.
 template <bool NORM>
-__global__ __launch_bounds__(256) void pf_pack_kernel(const float *X, int K, int n,
+__global__ __launch_bounds__(256) void pf_pack_kernel(const float *X, int K, int n, int nt,
                                                       const uint16_t *g, float eps, h8 *B) {
   const int t = blockIdx.x, tid = threadIdx.x;
   const float *x = X + (size_t)t * K;
@@ -67,17 +70,17 @@ __global__ __launch_bounds__(256) void pf_pack_kernel(const float *X, int K, int
       lo[e] = (_Float16)(y - (float)hi[e]);
     }
     B[(size_t)t * (K / 8) + kb] = hi;
-    B[(size_t)(PF_MAXT + t) * (K / 8) + kb] = lo;
+    B[(size_t)(nt + t) * (K / 8) + kb] = lo;
   }
 }
 
 // QKV outputs: interleaved rope of q and k at position pos0 + t
 // (src/shaders.ts:224-256), q -> Q[t][QD], k and v -> cache rows pos0 + t.
 // Grid: (n, QKV_ROWS / 2 / 256), one row pair per thread.
-__global__ void pf_qkv_epi_kernel(const float *C, float *Q, void *kc, void *vc, int kv_f32,
+__global__ void pf_qkv_epi_kernel(const float *C, int nt, float *Q, void *kc, void *vc, int kv_f32,
                                   int max_seq, int pos0, const float *inv_freq) {
   const int t = blockIdx.x, row = 2 * (blockIdx.y * blockDim.x + threadIdx.x);
-  const float y0 = pf_c(C, QKV_ROWS, t, row), y1 = pf_c(C, QKV_ROWS, t, row + 1);
+  const float y0 = pf_c(C, QKV_ROWS, nt, t, row), y1 = pf_c(C, QKV_ROWS, nt, t, row + 1);
   const int pos = pos0 + t;
   if (row < QD + KVD) {
     const float ang = (float)pos * inv_freq[(row & (HD - 1)) >> 1];
@@ -95,16 +98,16 @@ __global__ void pf_qkv_epi_kernel(const float *C, float *Q, void *kc, void *vc, 
 }
 
 // X[t][m] += output (m < M).  Grid: (n, M / 256).
-__global__ void pf_resid_epi_kernel(const float *C, int M, float *X) {
+__global__ void pf_resid_epi_kernel(const float *C, int M, int nt, float *X) {
   const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
-  X[(size_t)t * M + m] += pf_c(C, M, t, m);
+  X[(size_t)t * M + m] += pf_c(C, M, nt, t, m);
 }
 
 // act[t][m] = silu(gate) * up for the stacked [W1; W3] output (ldc = 2 HID).
 // Grid: (n, HID / 256).
-__global__ void pf_swiglu_epi_kernel(const float *C, float *act) {
+__global__ void pf_swiglu_epi_kernel(const float *C, int nt, float *act) {
   const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
-  const float gt = pf_c(C, 2 * HID, t, m), up = pf_c(C, 2 * HID, t, HID + m);
+  const float gt = pf_c(C, 2 * HID, nt, t, m), up = pf_c(C, 2 * HID, nt, t, HID + m);
   act[(size_t)t * HID + m] = (gt / (1.0f + expf(-gt))) * up;
 }
 
