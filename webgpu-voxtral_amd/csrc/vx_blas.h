@@ -6,12 +6,19 @@
 // products, so they go to the library; the per-token epilogues stay
 // hand-written.
 //
-// One plan per (M, K, N): on first use the heuristic's candidates are each
-// timed on the caller's stream and the fastest is kept.
+// One plan per (M, K, N), made on first use.  By default it is the
+// heuristic's first candidate: that choice depends only on the library and
+// the device, so every process computes bit-identical products (different
+// algorithms sum K in different orders).  With `tune`, the heuristic's
+// candidates are each timed on the caller's stream and the fastest is kept,
+// which may differ from process to process.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstdio>
+#include <cstdlib>
 #include <map>
 #include <string>
 #include <tuple>
@@ -23,8 +30,11 @@ class BlasGemm {
   ~BlasGemm() { release(); }
 
   // "" on success, else the failing call
-  std::string init(size_t workspace_bytes) {
+  std::string init(size_t workspace_bytes, bool tune) {
     if (h_) return "";
+    tune_ = tune;
+    const char *lg = getenv("VX_BLAS_LOG");  // print each new plan's algorithm on stderr
+    log_ = lg && atoi(lg) != 0;
     if (hipblasLtCreate(&h_) != HIPBLAS_STATUS_SUCCESS) {
       h_ = nullptr;
       return "hipblasLtCreate failed";
@@ -38,12 +48,7 @@ class BlasGemm {
   }
 
   void release() {
-    for (auto &p : plans_) {
-      hipblasLtMatrixLayoutDestroy(p.second.la);
-      hipblasLtMatrixLayoutDestroy(p.second.lb);
-      hipblasLtMatrixLayoutDestroy(p.second.lc);
-      hipblasLtMatmulDescDestroy(p.second.d);
-    }
+    for (auto &p : plans_) destroy(p.second);
     plans_.clear();
     if (ws_) (void)hipFree(ws_);
     ws_ = nullptr;
@@ -71,7 +76,14 @@ class BlasGemm {
     hipblasLtMatrixLayout_t la, lb, lc;
     hipblasLtMatmulAlgo_t algo;
   };
+  static void destroy(Plan &p) {
+    if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
+    if (p.lb) hipblasLtMatrixLayoutDestroy(p.lb);
+    if (p.lc) hipblasLtMatrixLayoutDestroy(p.lc);
+    if (p.d) hipblasLtMatmulDescDestroy(p.d);
+  }
   hipblasLtHandle_t h_ = nullptr;
+  bool tune_ = false, log_ = false;
   void *ws_ = nullptr;
   size_t wsz_ = 0;
   std::map<std::tuple<int, int, int>, Plan> plans_;
@@ -95,19 +107,33 @@ class BlasGemm {
             HIPBLAS_STATUS_SUCCESS ||
         hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16F, K, M, K) != HIPBLAS_STATUS_SUCCESS ||
         hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16F, K, N, K) != HIPBLAS_STATUS_SUCCESS ||
-        hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, M, N, M) != HIPBLAS_STATUS_SUCCESS)
+        hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, M, N, M) != HIPBLAS_STATUS_SUCCESS) {
+      destroy(p);
       return "hipBLASLt descriptor creation failed";
+    }
     hipblasLtMatmulPreference_t pref;
-    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return "preference";
+    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) {
+      destroy(p);
+      return "hipBLASLt preference creation failed";
+    }
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz_,
                                           sizeof wsz_);
     constexpr int NC = 8;
     hipblasLtMatmulHeuristicResult_t res[NC];
     int got = 0;
-    const hipblasStatus_t hs =
-        hipblasLtMatmulAlgoGetHeuristic(h_, p.d, p.la, p.lb, p.lc, p.lc, pref, NC, res, &got);
+    const hipblasStatus_t hs = hipblasLtMatmulAlgoGetHeuristic(h_, p.d, p.la, p.lb, p.lc, p.lc,
+                                                               pref, tune_ ? NC : 1, res, &got);
     hipblasLtMatmulPreferenceDestroy(pref);
-    if (hs != HIPBLAS_STATUS_SUCCESS || got < 1) return "no hipBLASLt algorithm for this GEMM";
+    if (hs != HIPBLAS_STATUS_SUCCESS || got < 1) {
+      destroy(p);
+      return "no hipBLASLt algorithm for this GEMM";
+    }
+    if (!tune_) {
+      p.algo = res[0].algo;
+      note(M, K, N, p.algo);
+      *out = &(plans_[key] = p);
+      return "";
+    }
     // time each candidate (on the real operands; C is overwritten later)
     hipEvent_t e0, e1;
     (void)hipEventCreate(&e0);
@@ -134,10 +160,21 @@ class BlasGemm {
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    if (bi < 0) return "every hipBLASLt candidate failed";
+    if (bi < 0) {
+      destroy(p);
+      return "every hipBLASLt candidate failed";
+    }
     p.algo = res[bi].algo;
+    note(M, K, N, p.algo);
     *out = &(plans_[key] = p);
     return "";
+  }
+
+  void note(int M, int K, int N, hipblasLtMatmulAlgo_t &algo) {
+    if (!log_) return;
+    fprintf(stderr, "[blas] M %d K %d N %d -> algorithm %d %s\n", M, K, N,
+            hipblaslt_ext::getIndexFromAlgo(algo),
+            hipblaslt_ext::getKernelNameFromAlgo(h_, algo).c_str());
   }
 };
 

@@ -781,7 +781,7 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
       *q.first = p;
       p += align256(q.second);
     }
-    if (const char *ch = getenv("VX_CODEC_CHUNK")) {  // (codec engines only)  // tokens per codec GEMM (tuning, tests)
+    if (const char *ch = getenv("VX_CODEC_CHUNK")) {  // tokens per codec GEMM (tuning, tests)
       const int v = atoi(ch);
       if (v >= 128 && v <= CX_MAXT && v % 128 == 0) e->cx_chunk = v;
     }
@@ -1352,7 +1352,10 @@ int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos) {
 // after n single steps.
 static int blas_setup(vx_engine *e) {
   if (e->blas_ready) return VX_OK;
-  const std::string err = e->blas.init(size_t(64) << 20);
+  // VX_BLAS_TUNE=1 times the library's candidates per GEMM shape (faster
+  // on some shapes, but the pick, and so the rounding, can vary per process)
+  const char *tune = getenv("VX_BLAS_TUNE");
+  const std::string err = e->blas.init(size_t(64) << 20, tune && atoi(tune) != 0);
   if (!err.empty()) return fail(e, VX_E_DEVICE, "%s", err.c_str());
   e->blas_ready = true;
   return VX_OK;
