@@ -229,14 +229,15 @@ GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, in
 
 }  // namespace
 
-// FM GEMM launch: `rows` output rows in tiles of 16, RG tiles per block.
+// FM GEMM launch: `rows` output rows in tiles of FTR, RG tiles per block.
 template <int EPI, int K, int RG, int KS, int P>
 void launch_gemm6(hipStream_t st, const Gemm6Args &a, int rows) {
-  hipLaunchKernelGGL((gemm6_kernel<EPI, K, RG, KS, P>), dim3(rows / (16 * RG)), dim3(RG * KS * 64),
+  hipLaunchKernelGGL((gemm6_kernel<EPI, K, RG, KS, P>), dim3(rows / (FTR * RG)), dim3(RG * KS * 64),
                      0, st, a);
 }
-static_assert(QKV_ROWS % 16 == 0 && DIM % 16 == 0 && HID % 16 == 0 && DIM / 16 <= SSQ_MAX &&
-                  DIM % 256 == 0,
+// 12-row tiles divide every FM matrix into a multiple of 256 tiles
+static_assert(QKV_ROWS % (256 * FTR) == 0 && DIM % (256 * FTR) == 0 && HID % (256 * FTR) == 0 &&
+                  DIM / FTR <= SSQ_MAX && DIM % 256 == 0,
               "FM GEMM tiles");
 
 // Streaming GEMV launch: M units split exactly into blocks of WAVES*UPW.
@@ -374,7 +375,7 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
         a.out = e->fm_q;
         a.out_k = e->fm_k;
         a.out_v = e->fm_v;
-        launch_gemm6<EPI_QKV, DIM, 1, 2, 12>(st, a, QKV_ROWS);
+        launch_gemm6<EPI_QKV, DIM, 1, 8, 4>(st, a, QKV_ROWS);
       }
       hipLaunchKernelGGL(fm_attn_kernel, dim3(NH, 2), dim3(64), 0, st, e->fm_q, e->fm_k, e->fm_v,
                          e->fm_attn, e->fm_b_o);
@@ -387,7 +388,7 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
         a.Bn = e->fm_b_ffn;
         a.gn = W.ffn_norm;
         a.ssq_out = e->fm_ssq_ffn;
-        launch_gemm6<EPI_RESID, QD, 1, 4, 16>(st, a, DIM);
+        launch_gemm6<EPI_RESID, QD, 1, 16, 4>(st, a, DIM);
       }
       {  // RMSNorm + gate/up + SwiGLU; hands the activation to down
         Gemm6Args a{};
@@ -395,7 +396,7 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
         a.W2 = P.w3;
         a.B = e->fm_b_ffn;
         a.ssq = e->fm_ssq_ffn;
-        a.nssq = DIM / 16;
+        a.nssq = DIM / FTR;
         a.eps = 1e-5f;
         a.out = e->fm_act;
         a.os = HID;
@@ -413,8 +414,8 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
           a.gn = e->FL[l + 1].attn_norm;
           a.ssq_out = e->fm_ssq_attn;
         }
-        launch_gemm6<EPI_RESID, HID, 1, 4, 24>(st, a, DIM);
-        nssq_attn = DIM / 16;
+        launch_gemm6<EPI_RESID, HID, 1, 12, 12>(st, a, DIM);
+        nssq_attn = DIM / FTR;
       }
     }
     {  // final norm of position 0 of each branch -> acoustic_out -> vel[s]

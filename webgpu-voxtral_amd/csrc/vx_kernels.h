@@ -726,14 +726,18 @@ __global__ void gen_kv_kernel(KVT *cache, int max_seq, int npos, uint64_t seed, 
 // sequence positions x conditional/unconditional), so its GEMVs are thin
 // GEMMs, out[v][row] = sum_k W[row][k] * y[v][k], run on
 // v_mfma_f32_16x16x32_f16:
-//  - A operand: the weights, pre-arranged once as [row tile][k chunk][lane][8]
-//    (rows t*16 + lane%16, k = chunk*32 + (lane/16)*8 + e), so one chunk's
-//    operand is a contiguous 1 KB read;
+//  - A operand: the weights in tiles of FTR = 12 rows (every FM matrix has a
+//    multiple of 256 x 12 rows, so each of the 256 CUs gets the same number
+//    of tiles; 16-row tiles left 64 CUs idle on the 3072-row matrices),
+//    pre-arranged once as [row tile][k chunk][48][8]: entry g*12 + m holds
+//    row t*12 + m, k = chunk*32 + g*8 + e.  Lane l feeds MFMA row l%16 and k
+//    group l/16; lanes of rows 12-15 load nothing (zeros), so one chunk's
+//    operand is a contiguous 768-byte read;
 //  - B operand: the packed input [k/8][BCOL] of 8-half groups, column v the
 //    hi part f16(y_v) and column FMV+v the lo part f16(y_v - hi): W is exactly
 //    f16, so D[.][v] + D[.][FMV+v] is the f32 dot product up to rounding of
 //    order 2^-22 (f16 subnormals are kept by the conversion).  Columns 12-15
-//    of D are never read.
+//    and rows 12-15 of D are never read.
 // The kernel that produces a GEMM's input writes this packed form in its
 // epilogue, with the next RMSNorm's gains already applied; the RMS scale
 // itself multiplies the GEMM result (W.(x*g*r) = r * W.(x*g)), from
@@ -741,7 +745,8 @@ __global__ void gen_kv_kernel(KVT *cache, int max_seq, int npos, uint64_t seed, 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 constexpr int FMV = 6;
 constexpr int BCOL = 2 * FMV;
-constexpr int SSQ_MAX = 192;  // partial sums of squares per vector (row tiles of a DIM output)
+constexpr int FTR = 12;       // rows per FM weight tile
+constexpr int SSQ_MAX = 256;  // partial sums of squares per vector (row tiles of a DIM output)
 
 __device__ __forceinline__ void bpack_put(h8 *B, int v, int k, float y) {
   const _Float16 hi = (_Float16)y, lo = (_Float16)(y - (float)hi);
@@ -763,17 +768,18 @@ __device__ __forceinline__ void bpack_put4(h8 *B, int v, int k, f32x4 y) {
   *(h4 *)(p + (FMV + v) * 8 + (k & 7)) = lo;
 }
 
-// W [M][K] row-major -> [M/16][K/32][64][8] (see above)
+// W [M][K] row-major -> [M/12][K/32][48][8] (see above); M % 12 == 0
 __global__ void pack_mfma_a_kernel(const uint16_t *W, uint16_t *Wp, int M, int K) {
   const size_t total = (size_t)M * K / 8;
   const int nch = K / 32;
   for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
        q += (size_t)gridDim.x * blockDim.x) {
-    const int lane = (int)(q & 63);
-    const size_t tc = q >> 6;
+    const int e = (int)(q % (4 * FTR));
+    const size_t tc = q / (4 * FTR);
     const int c = (int)(tc % nch);
     const size_t tile = tc / nch;
-    const uint16_t *src = W + (tile * 16 + (lane & 15)) * K + c * 32 + (lane >> 4) * 8;
+    const int g = e / FTR, m = e - g * FTR;
+    const uint16_t *src = W + (tile * FTR + m) * K + c * 32 + g * 8;
     *(u32x4 *)(Wp + q * 8) = *(const u32x4 *)src;
   }
 }
@@ -794,7 +800,7 @@ struct Gemm6Args {
 
 // Block = RG row tiles x KS k-slices (one wave each); a wave streams its
 // tile's chunks (EPI_SWIGLU: the gate and up tiles), P chunks in flight, and
-// k-slices are summed through LDS.  Grid = rows / (16 RG).
+// k-slices are summed through LDS.  Grid = rows / (FTR RG).
 template <int EPI, int K, int RG, int KS, int P>
 __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
   constexpr int TL = EPI == EPI_SWIGLU ? 2 : 1;
@@ -803,10 +809,15 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
   __shared__ f32x4 part[KS > 1 ? (KS - 1) * RG * TL : 1][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rg = wave / KS, kp = wave % KS;
-  const int tile = blockIdx.x * RG + rg, row0 = tile * 16, n = lane & 15;
+  const int tile = blockIdx.x * RG + rg, row0 = tile * FTR, n = lane & 15;
+  // A-operand lanes of rows 12-15 load nothing; D rows 12-15 (lanes >= 48)
+  // are dropped
+  const bool arow = n < FTR, drow = (lane >> 4) < FTR / 4;
   const uint16_t *wp[TL];
 #pragma unroll
-  for (int t = 0; t < TL; t++) wp[t] = (t ? a.W2 : a.W) + ((size_t)tile * NC * 64 + lane) * 8;
+  for (int t = 0; t < TL; t++)
+    wp[t] = (t ? a.W2 : a.W) +
+            ((size_t)tile * NC * (4 * FTR) + (lane >> 4) * FTR + (arow ? n : 0)) * 8;
   // lanes of columns 12-15 read a duplicate column (their D columns are unused)
   const h8 *bp = a.B + (lane >> 4) * BCOL + (n < BCOL ? n : n - FMV);
   // RMS scale of each input vector from the producer's partial sums
@@ -825,7 +836,8 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
     const int c = kp * NCW + i;
     bb[d] = bp[c * 4 * BCOL];
 #pragma unroll
-    for (int t = 0; t < TL; t++) wb[d][t] = *(const u32x4 *)(wp[t] + (size_t)c * 512);
+    for (int t = 0; t < TL; t++)
+      wb[d][t] = arow ? *(const u32x4 *)(wp[t] + (size_t)c * (4 * FTR * 8)) : u32x4{0u, 0u, 0u, 0u};
   };
 #pragma unroll
   for (int d = 0; d < P; d++) load(d, d);
@@ -871,7 +883,8 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
 #pragma unroll
   for (int u = 1; u < FMV; u++) rv = v == u ? rs[u] : rv;
   f32x4 y = acc[0] * rv;  // new values of rows r..r+3 (EPI_RESID: after the add)
-  if (n < FMV) {
+  const bool live = n < FMV && drow;
+  if (live) {
     if (EPI == EPI_SWIGLU) {
       const f32x4 u = acc[TL - 1] * rv;
 #pragma unroll
@@ -893,10 +906,10 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
     }
   }
   if (a.Bn) {  // producer side of the next GEMM
-    float s2 = n < FMV ? y[0] * y[0] + y[1] * y[1] + y[2] * y[2] + y[3] * y[3] : 0.f;
+    float s2 = live ? y[0] * y[0] + y[1] * y[1] + y[2] * y[2] + y[3] * y[3] : 0.f;
     s2 += __shfl_xor(s2, 16, 64);
     s2 += __shfl_xor(s2, 32, 64);
-    if (n < FMV) {
+    if (live) {
       f32x4 z = y;
       if (a.gn)
 #pragma unroll
