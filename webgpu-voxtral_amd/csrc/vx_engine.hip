@@ -112,7 +112,7 @@ struct vx_engine {
   // batched prefill (vx_prefill.h): chunk activations, packed GEMM input,
   // GEMM output, the chunk's token ids and voice rows
   void *pf_arena = nullptr;
-  float *pf_x = nullptr, *pf_q = nullptr, *pf_attn = nullptr, *pf_act = nullptr, *pf_c = nullptr,
+  float *pf_x = nullptr, *pf_q = nullptr, *pf_c = nullptr,
         *pf_voice = nullptr;
   h8 *pf_b = nullptr;
   int32_t *pf_tok = nullptr;
@@ -797,8 +797,6 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
     std::vector<std::pair<void **, size_t>> parts = {
         {(void **)&e->pf_x, (size_t)PF_MAXT * DIM * 4},
         {(void **)&e->pf_q, (size_t)PF_MAXT * QD * 4},
-        {(void **)&e->pf_attn, (size_t)PF_MAXT * QD * 4},
-        {(void **)&e->pf_act, (size_t)PF_MAXT * HID * 4},
         {(void **)&e->pf_c, (size_t)PF_NC * 2 * HID * 4},
         {(void **)&e->pf_b, (size_t)HID / 8 * PF_NC * 16},
         {(void **)&e->pf_voice, (size_t)PF_MAXT * DIM * 4},
@@ -1378,35 +1376,35 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
   hipLaunchKernelGGL(pf_embed_kernel, dim3(n, DIM / 256), dim3(256), 0, st, e->tok_emb, e->pf_tok,
                      has_voice ? e->pf_voice : nullptr, vstart, vcount, tok0, e->pf_x);
   const dim3 blk(256);
+  // layer 0's B; every later B is written by the kernel producing its input
+  hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(nt), blk, 0, st, e->pf_x, DIM, n, nt,
+                     e->L[0].attn_norm, e->cfg.norm_eps, e->pf_b);
   for (int l = 0; l < e->cfg.n_layers; l++) {
     const LayerW &W = e->L[l];
-    hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(nt), blk, 0, st, e->pf_x, DIM, n, nt,
-                       W.attn_norm, e->cfg.norm_eps, e->pf_b);
+    const bool next = l + 1 < e->cfg.n_layers;
     if ((rc = blas_gemm(e, W.wqkv, QKV_ROWS, DIM, e->pf_b, N, e->pf_c))) return rc;
     hipLaunchKernelGGL(pf_qkv_epi_kernel, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c, nt,
                        e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
     if (e->kv_f32)
-      hipLaunchKernelGGL(pf_attn_kernel<float>, dim3(n, NKV), blk, 0, st, e->pf_q, e->kc(l),
-                         e->vc(l), e->max_seq, pos0, e->pf_attn);
+      hipLaunchKernelGGL(pf_attn_kernel<float>, dim3(nt, NKV), blk, 0, st, e->pf_q, e->kc(l),
+                         e->vc(l), e->max_seq, pos0, n, nt, e->pf_b);
     else
-      hipLaunchKernelGGL(pf_attn_kernel<uint16_t>, dim3(n, NKV), blk, 0, st, e->pf_q, e->kc(l),
-                         e->vc(l), e->max_seq, pos0, e->pf_attn);
-    hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(nt), blk, 0, st, e->pf_attn, QD, n, nt,
-                       nullptr, 0.f, e->pf_b);
+      hipLaunchKernelGGL(pf_attn_kernel<uint16_t>, dim3(nt, NKV), blk, 0, st, e->pf_q, e->kc(l),
+                         e->vc(l), e->max_seq, pos0, n, nt, e->pf_b);
     if ((rc = blas_gemm(e, W.wo, DIM, QD, e->pf_b, N, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, nt,
-                       e->pf_x);
-    hipLaunchKernelGGL(pf_pack_kernel<true>, dim3(nt), blk, 0, st, e->pf_x, DIM, n, nt,
+    hipLaunchKernelGGL(pf_resid_pack_kernel<true>, dim3(nt), blk, 0, st, e->pf_c, n, nt, e->pf_x,
                        W.ffn_norm, e->cfg.norm_eps, e->pf_b);
     // W1 and W3 are adjacent in the arena: one GEMM over the stacked rows
     if ((rc = blas_gemm(e, W.w1, 2 * HID, DIM, e->pf_b, N, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_swiglu_epi_kernel, dim3(n, HID / 256), blk, 0, st, e->pf_c, nt,
-                       e->pf_act);
-    hipLaunchKernelGGL(pf_pack_kernel<false>, dim3(nt), blk, 0, st, e->pf_act, HID, n, nt,
-                       nullptr, 0.f, e->pf_b);
+    hipLaunchKernelGGL(pf_swiglu_pack_kernel, dim3(nt, HID / 8 / 128), dim3(128), 0, st, e->pf_c,
+                       n, nt, e->pf_b);
     if ((rc = blas_gemm(e, W.w2, DIM, HID, e->pf_b, N, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_resid_epi_kernel, dim3(n, DIM / 256), blk, 0, st, e->pf_c, DIM, nt,
-                       e->pf_x);
+    if (next)
+      hipLaunchKernelGGL(pf_resid_pack_kernel<true>, dim3(nt), blk, 0, st, e->pf_c, n, nt,
+                         e->pf_x, e->L[l + 1].attn_norm, e->cfg.norm_eps, e->pf_b);
+    else
+      hipLaunchKernelGGL(pf_resid_pack_kernel<false>, dim3(n), blk, 0, st, e->pf_c, n, nt,
+                         e->pf_x, nullptr, 0.f, nullptr);
   }
   (void)hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * DIM, DIM * 4, hipMemcpyDeviceToDevice, st);
   hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, e->x, e->final_norm,

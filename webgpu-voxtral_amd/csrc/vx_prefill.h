@@ -5,10 +5,11 @@
 //   C[col][m] = sum_k W[m][k] * B[col][k]
 // (f16 x f16 -> f32 on the matrix cores, through hipBLASLt: vx_blas.h).  W
 // is the layer's f16 weight matrix (row-major, as loaded); B holds the
-// chunk's activations in hi/lo form (column t = f16(y_t), column
-// PF_MAXT + t = f16(y_t - hi), each column's K halves contiguous), so the
-// product keeps f32 accuracy.  Small per-token kernels do RMSNorm + packing,
-// RoPE + K/V writes, residual adds, SwiGLU and the causal attention.  The
+// chunk's activations in hi/lo form (column t = f16(y_t), column nt + t =
+// f16(y_t - hi), each column's K halves contiguous), so the product keeps
+// f32 accuracy.  Small per-token kernels do RoPE + K/V writes and the causal
+// attention, and each of them, or a residual add + RMSNorm, or SwiGLU,
+// writes the next GEMM's B directly.  The
 // result (K/V cache rows, residual stream, final norm of the last token,
 // position) equals that of the per-token steps up to f32 summation order.
 #pragma once
@@ -97,30 +98,118 @@ __global__ void pf_qkv_epi_kernel(const float *C, int nt, float *Q, void *kc, vo
   }
 }
 
-// X[t][m] += output (m < M).  Grid: (n, M / 256).
-__global__ void pf_resid_epi_kernel(const float *C, int M, int nt, float *X) {
-  const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
-  X[(size_t)t * M + m] += pf_c(C, M, nt, t, m);
+// hi/lo halves of y into B columns t and nt + t at k (8 consecutive k)
+__device__ __forceinline__ void pf_put8(h8 *B, int K, int nt, int t, int kb, const float (&y)[8]) {
+  h8 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    hi[e] = (_Float16)y[e];
+    lo[e] = (_Float16)(y[e] - (float)hi[e]);
+  }
+  B[(size_t)t * (K / 8) + kb] = hi;
+  B[(size_t)(nt + t) * (K / 8) + kb] = lo;
 }
 
-// act[t][m] = silu(gate) * up for the stacked [W1; W3] output (ldc = 2 HID).
-// Grid: (n, HID / 256).
-__global__ void pf_swiglu_epi_kernel(const float *C, int nt, float *act) {
-  const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
-  const float gt = pf_c(C, 2 * HID, nt, t, m), up = pf_c(C, 2 * HID, nt, t, HID + m);
-  act[(size_t)t * HID + m] = (gt / (1.0f + expf(-gt))) * up;
+// Residual add of a DIM-row GEMM output, X[t] += y (addInPlace,
+// src/shaders.ts:532-547), then, with PACK, the next GEMM's B from
+// rmsNorm(X[t]) * g (src/shaders.ts:137-183); columns of tokens t >= n are
+// zero.  Grid: nt blocks (n without PACK) of 256; thread i owns the 8-value
+// groups i and i + 256 (DIM / 8 = 384 groups).
+template <bool PACK>
+__global__ __launch_bounds__(256) void pf_resid_pack_kernel(const float *C, int n, int nt, float *X,
+                                                            const uint16_t *g, float eps, h8 *B) {
+  constexpr int NG = DIM / 8, GPT = (NG + 255) / 256;
+  const int t = blockIdx.x, tid = threadIdx.x;
+  float v[GPT][8];
+  float ss = 0.f;
+  if (t < n) {
+#pragma unroll
+    for (int i = 0; i < GPT; i++) {
+      const int kb = tid + 256 * i;
+      if (kb < NG) {
+        float *x = X + (size_t)t * DIM + kb * 8;
+        const float *ch = C + (size_t)t * DIM + kb * 8, *cl = C + (size_t)(nt + t) * DIM + kb * 8;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const f32x4 xv = *(const f32x4 *)(x + 4 * h), a = *(const f32x4 *)(ch + 4 * h),
+                      b = *(const f32x4 *)(cl + 4 * h);
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[i][4 * h + e] = xv[e] + (a[e] + b[e]);
+          *(f32x4 *)(x + 4 * h) = f32x4{v[i][4 * h], v[i][4 * h + 1], v[i][4 * h + 2], v[i][4 * h + 3]};
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) ss = fmaf(v[i][e], v[i][e], ss);
+      }
+    }
+  }
+  if (!PACK) return;
+  float r = 0.f;
+  if (t < n) {
+    __shared__ float red[4];
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    r = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)DIM + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < GPT; i++) {
+    const int kb = tid + 256 * i;
+    if (kb < NG) {
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) y[e] = t < n ? v[i][e] * r * h2f(g[kb * 8 + e]) : 0.f;
+      pf_put8(B, DIM, nt, t, kb, y);
+    }
+  }
 }
+
+// SwiGLU of the stacked [W1; W3] output (ldc = 2 HID; swiGLU,
+// src/shaders.ts:483-501) written as the down GEMM's B (K = HID); columns of
+// tokens t >= n are zero.  Grid: (nt, HID / 8 / 128) of 128, one 8-value
+// group per thread.
+__global__ __launch_bounds__(128) void pf_swiglu_pack_kernel(const float *C, int n, int nt, h8 *B) {
+  const int t = blockIdx.x, kb = blockIdx.y * 128 + threadIdx.x;
+  float y[8];
+  if (t < n) {
+    const size_t ld = 2 * HID;
+    const float *gh = C + (size_t)t * ld + kb * 8, *gl = C + (size_t)(nt + t) * ld + kb * 8;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const f32x4 a = *(const f32x4 *)(gh + 4 * h), b = *(const f32x4 *)(gl + 4 * h);
+      const f32x4 c = *(const f32x4 *)(gh + HID + 4 * h), d = *(const f32x4 *)(gl + HID + 4 * h);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float gt = a[e] + b[e], up = c[e] + d[e];
+        y[4 * h + e] = (gt / (1.0f + expf(-gt))) * up;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++) y[e] = 0.f;
+  }
+  pf_put8(B, HID, nt, t, kb, y);
+}
+static_assert(DIM % 8 == 0 && (HID / 8) % 128 == 0, "prefill packing groups");
 
 // Causal attention of the chunk: query t (position pos0 + t) over keys
-// 0..pos0 + t of the cache.  Grid (n, NKV), 4 waves = the 4 query heads of
-// the KV head; keys in LDS tiles of AT_T with an online softmax.
+// 0..pos0 + t of the cache.  Grid (nt, NKV), 4 waves = the 4 query heads of
+// the KV head; keys in LDS tiles of AT_T with an online softmax.  The result
+// goes to the O GEMM's B (K = QD) in hi/lo form; blocks of tokens t >= n
+// write zero columns.
 template <typename KVT>
 __global__ __launch_bounds__(256) void pf_attn_kernel(const float *Q, const void *kc, const void *vc,
-                                                      int max_seq, int pos0, float *out) {
+                                                      int max_seq, int pos0, int n, int nt, h8 *B) {
   using G = KvTile<KVT>;
   const int t = blockIdx.x, kvh = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = kvh * (NH / NKV) + wave;
+  _Float16 *bh = (_Float16 *)B + (size_t)t * QD + h * HD + lane * 2;
+  _Float16 *bl = (_Float16 *)B + (size_t)(nt + t) * QD + h * HD + lane * 2;
+  if (t >= n) {
+    *(uint32_t *)bh = 0u;
+    *(uint32_t *)bl = 0u;
+    return;
+  }
   const int p1 = pos0 + t + 1;
   __shared__ __attribute__((aligned(16))) float qs[4][HD];
   __shared__ __attribute__((aligned(16))) KVT ks[AT_T * G::LDW];
@@ -171,8 +260,12 @@ __global__ __launch_bounds__(256) void pf_attn_kernel(const float *Q, const void
       o1 = fmaf(ej, v.y, o1);
     }
   }
-  out[(size_t)t * QD + h * HD + lane * 2] = o0 / l;
-  out[(size_t)t * QD + h * HD + lane * 2 + 1] = o1 / l;
+  const float y0 = o0 / l, y1 = o1 / l;
+  const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+  const _Float16 l0 = (_Float16)(y0 - (float)h0), l1 = (_Float16)(y1 - (float)h1);
+  typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
+  *(hh2 *)bh = hh2{h0, h1};
+  *(hh2 *)bl = hh2{l0, l1};
 }
 
 }  // namespace vx
