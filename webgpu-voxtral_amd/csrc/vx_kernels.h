@@ -380,12 +380,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(GemvArgs a) {
   float resid[UPW];
 #pragma unroll
   for (int u = 0; u < UPW; u++) resid[u] = EPI == EPI_RESID ? a.out[u0 + u] : 0.f;
+  // when the threads tile K exactly the guard is known true at compile
+  // time: an unconditional load lets the compiler issue the weight loads
+  // right behind it instead of waiting on it inside a branch
+  constexpr bool XEXACT = K % (NT * 4) == 0;
   f32x4 xv[XPT];
   uint2 gv[XPT];
 #pragma unroll
   for (int i = 0; i < XPT; i++) {
     const int k = (tid + i * NT) * 4;
-    if (k < K) {
+    if (XEXACT || k < K) {
       xv[i] = *(const f32x4 *)(a.x + k);
       if (NORM) gv[i] = *(const uint2 *)(a.norm_w + k);
     }
@@ -400,7 +404,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(GemvArgs a) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < XPT; i++)
-      if ((tid + i * NT) * 4 < K)
+      if (XEXACT || (tid + i * NT) * 4 < K)
         s += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
     s = wave_sum(s);
     if (lane == 0) red[wave] = s;
@@ -413,7 +417,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(GemvArgs a) {
 #pragma unroll
   for (int i = 0; i < XPT; i++) {
     const int k = (tid + i * NT) * 4;
-    if (k < K) {
+    if (XEXACT || k < K) {
       f32x4 v = xv[i];
       if (NORM) {
         const h2 g01 = __builtin_bit_cast(h2, gv[i].x), g23 = __builtin_bit_cast(h2, gv[i].y);
@@ -807,7 +811,7 @@ struct Gemm6Args {
   float *out_k, *out_v;    // EPI_QKV
   h8 *Bn;                  // optional: next GEMM's packed input from the new values
   const uint16_t *gn;      //   times these gains (null: none)
-  float *ssq_out;          //   and their sums of squares per (row tile, vector)
+  float *ssq_out;          //   and their sums of squares, vector-major [FMV][SSQ_MAX]
 };
 
 // Block = RG row tiles x KS k-slices (one wave each); a wave streams its
@@ -822,26 +826,29 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rg = wave / KS, kp = wave % KS;
   const int tile = blockIdx.x * RG + rg, row0 = tile * FTR, n = lane & 15;
-  // A-operand lanes of rows 12-15 load nothing; D rows 12-15 (lanes >= 48)
-  // are dropped
-  const bool arow = n < FTR, drow = (lane >> 4) < FTR / 4;
+  // A-operand lanes of rows 12-15 re-read rows 8-11 (the same cache lines,
+  // so no extra traffic): rows of D depend only on the same rows of A, and
+  // D rows 12-15 (lanes >= 48) are dropped.  The loads stay unconditional,
+  // so the compiler issues them back to back.
+  const bool drow = (lane >> 4) < FTR / 4;
   const uint16_t *wp[TL];
 #pragma unroll
   for (int t = 0; t < TL; t++)
     wp[t] = (t ? a.W2 : a.W) +
-            ((size_t)tile * NC * (4 * FTR) + (lane >> 4) * FTR + (arow ? n : 0)) * 8;
+            ((size_t)tile * NC * (4 * FTR) + (lane >> 4) * FTR + (n < FTR ? n : n - 4)) * 8;
   // lanes of columns 12-15 read a duplicate column (their D columns are unused)
   const h8 *bp = a.B + (lane >> 4) * BCOL + (n < BCOL ? n : n - FMV);
   // RMS scale of each input vector from the producer's partial sums
-  // (at most SSQ_MAX per vector); loaded before the weights, whose loads
-  // return after them
-  float sv[SSQ_MAX / 64][FMV];
-  const bool norm = a.ssq != nullptr && kp == 0;
+  // (nssq <= SSQ_MAX per vector, vector-major): one contiguous 16-byte load
+  // per vector and lane, issued before the weights, whose loads return after
+  // them.  Entries past nssq are masked (the buffer is shared by producers
+  // of different partial counts).
+  f32x4 sv[FMV];
+  const bool norm = a.ssq != nullptr && kp == 0;  // wave-uniform
+  if (norm) {
 #pragma unroll
-  for (int i = 0; i < SSQ_MAX / 64; i++)
-#pragma unroll
-    for (int v = 0; v < FMV; v++)
-      sv[i][v] = norm && lane + 64 * i < a.nssq ? a.ssq[(lane + 64 * i) * FMV + v] : 0.f;
+    for (int v = 0; v < FMV; v++) sv[v] = *(const f32x4 *)(a.ssq + v * SSQ_MAX + lane * 4);
+  }
   u32x4 wb[P][TL];
   h8 bb[P];
   auto load = [&](int i, int d) {
@@ -849,17 +856,21 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
     bb[d] = bp[c * 4 * BCOL];
 #pragma unroll
     for (int t = 0; t < TL; t++)
-      wb[d][t] = arow ? ldw(wp[t] + (size_t)c * (4 * FTR * 8)) : u32x4{0u, 0u, 0u, 0u};
+      wb[d][t] = ldw(wp[t] + (size_t)c * (4 * FTR * 8));
   };
 #pragma unroll
   for (int d = 0; d < P; d++) load(d, d);
   float rs[FMV];
 #pragma unroll
-  for (int v = 0; v < FMV; v++) {
-    float s = 0.f;
+  for (int v = 0; v < FMV; v++) rs[v] = 1.0f;
+  if (norm) {
 #pragma unroll
-    for (int i = 0; i < SSQ_MAX / 64; i++) s += sv[i][v];
-    rs[v] = norm ? 1.0f / sqrtf(wave_sum(s) / (float)DIM + a.eps) : 1.0f;
+    for (int v = 0; v < FMV; v++) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) s += lane * 4 + j < a.nssq ? sv[v][j] : 0.f;
+      rs[v] = 1.0f / sqrtf(wave_sum(s) / (float)DIM + a.eps);
+    }
   }
   f32x4 acc[TL];
 #pragma unroll
@@ -927,7 +938,7 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
 #pragma unroll
         for (int j = 0; j < 4; j++) z[j] *= h2f(a.gn[r + j]);
       bpack_put4(a.Bn, v, r, z);
-      if (a.ssq_out && lane < 16) a.ssq_out[tile * FMV + v] = s2;
+      if (a.ssq_out && lane < 16) a.ssq_out[v * SSQ_MAX + tile] = s2;
     }
   }
 }
@@ -1159,7 +1170,7 @@ struct FmStepArgs {
   const float *noise;    // step 0: x_t = noise
   h8 *Bn;                // packed input of the first layer's QKV GEMM,
   const uint16_t *gn;    //   times its attention-norm gains,
-  float *ssq_out;        //   and sums of squares [block][FMV]
+  float *ssq_out;        //   and sums of squares, vector-major [FMV][SSQ_MAX]
 };
 
 // Start of Euler step s: x_s (from x_{s-1} and the CFG velocity of step
@@ -1197,7 +1208,7 @@ __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
     if ((t & 63) == 0) red[t >> 6][v] = s2;
   }
   __syncthreads();
-  if (t < FMV) a.ssq_out[blockIdx.x * FMV + t] = red[0][t] + red[1][t] + red[2][t] + red[3][t];
+  if (t < FMV) a.ssq_out[t * SSQ_MAX + blockIdx.x] = red[0][t] + red[1][t] + red[2][t] + red[3][t];
 }
 
 // Bidirectional 3-token GQA attention of both CFG branches: grid (NH, 2),
