@@ -170,84 +170,98 @@ __device__ __forceinline__ void kv_store2(void *cache, int kv_f32, int max_seq, 
 // row per load instruction.
 template <int NB, int WAVES, int RPW, int EPI, bool NORM, int K, int KT>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
-  static_assert(K % KT == 0 && KT % 512 == 0 && EPI != EPI_QKV_ROPE, "tile");
+  static_assert(KT == K && K % 512 == 0 && EPI != EPI_QKV_ROPE, "one K tile");
   constexpr int NT = WAVES * 64;
-  constexpr int NCH = KT / 512;
-  __shared__ __attribute__((aligned(16))) float xl[NB * KT];
+  constexpr int NCH = K / 512;
+  static_assert(K % (NT * 4) == 0, "threads tile K");
+  constexpr int XPV = K / (NT * 4);  // float4s of one input vector per thread
+  __shared__ __attribute__((aligned(16))) float xl[NB * K];
   __shared__ float red[WAVES][NB];
-  __shared__ float scl[NB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int unit0 = (blockIdx.x * WAVES + wave) * (EPI == EPI_SWIGLU ? RPW / 2 : RPW);
+  const bool active = unit0 < a.M;
 
+  // input vectors (and RMSNorm gains) first, then the weights: per-wave
+  // loads return in issue order, so the prologue below waits only on the
+  // former while the weights are in flight
+  f32x4 xv[NB][XPV];
+  uint2 gv[XPV];
+#pragma unroll
+  for (int i = 0; i < XPV; i++) {
+    const int k = (tid + i * NT) * 4;
+#pragma unroll
+    for (int b = 0; b < NB; b++) xv[b][i] = *(const f32x4 *)(a.x + (size_t)b * a.xs + k);
+    if (NORM) gv[i] = *(const uint2 *)(a.norm_w + k);
+  }
+  u32x4 w[RPW][NCH];
+#pragma unroll
+  for (int r = 0; r < RPW; r++) {
+    const uint16_t *rowp;
+    if (EPI == EPI_SWIGLU)
+      rowp = ((r & 1) ? a.W2 : a.W) + (size_t)min(unit0 + (r >> 1), a.M - 1) * K;
+    else
+      rowp = a.W + (size_t)min(unit0 + r, a.M - 1) * K;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) w[r][c] = ldw(rowp + c * 512 + lane * 8);
+  }
+
+  float scl[NB];
+#pragma unroll
+  for (int b = 0; b < NB; b++) scl[b] = 1.0f;
   if (NORM) {  // rmsNorm prologue: rms = 1/sqrt(mean(x^2) + eps)
-    float ss[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) {
       float s = 0.f;
-      for (int i = tid * 4; i < K; i += NT * 4) {
-        f32x4 v = *(const f32x4 *)(a.x + (size_t)b * a.xs + i);
-        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-      }
-      ss[b] = wave_sum(s);
-    }
-    if (lane == 0)
 #pragma unroll
-      for (int b = 0; b < NB; b++) red[wave][b] = ss[b];
+      for (int i = 0; i < XPV; i++)
+        s += xv[b][i].x * xv[b][i].x + xv[b][i].y * xv[b][i].y + xv[b][i].z * xv[b][i].z +
+             xv[b][i].w * xv[b][i].w;
+      s = wave_sum(s);
+      if (lane == 0) red[wave][b] = s;
+    }
     __syncthreads();
-    if (tid < NB) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
       float s = 0.f;
 #pragma unroll
-      for (int w = 0; w < WAVES; w++) s += red[w][tid];
-      scl[tid] = 1.0f / sqrtf(s / (float)K + a.eps);
+      for (int q = 0; q < WAVES; q++) s += red[q][b];
+      scl[b] = 1.0f / sqrtf(s / (float)K + a.eps);
     }
-    __syncthreads();
   }
+#pragma unroll
+  for (int i = 0; i < XPV; i++) {
+    const int k = (tid + i * NT) * 4;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      f32x4 v = xv[b][i];
+      if (NORM) {
+        const float r = scl[b];
+        const h2 g01 = __builtin_bit_cast(h2, gv[i].x), g23 = __builtin_bit_cast(h2, gv[i].y);
+        v.x = v.x * r * (float)g01.x;
+        v.y = v.y * r * (float)g01.y;
+        v.z = v.z * r * (float)g23.x;
+        v.w = v.w * r * (float)g23.y;
+      }
+      *(f32x4 *)(xl + b * K + k) = v;
+    }
+  }
+  __syncthreads();
 
   float acc[RPW][NB];
 #pragma unroll
   for (int r = 0; r < RPW; r++)
 #pragma unroll
     for (int b = 0; b < NB; b++) acc[r][b] = 0.f;
-
-  const bool active = unit0 < a.M;
-  for (int kt = 0; kt < K; kt += KT) {
-    if (kt) __syncthreads();
-    for (int i = tid * 4; i < NB * KT; i += NT * 4) {
-      int b = i / KT, k = i - b * KT;
-      f32x4 v = *(const f32x4 *)(a.x + (size_t)b * a.xs + kt + k);
-      if (NORM) {
-        float r = scl[b];
-        const uint16_t *g = a.norm_w + kt + k;
-        v.x = v.x * r * h2f(g[0]);
-        v.y = v.y * r * h2f(g[1]);
-        v.z = v.z * r * h2f(g[2]);
-        v.w = v.w * r * h2f(g[3]);
+  if (active) {
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+#pragma unroll
+      for (int b = 0; b < NB; b++) {
+        const float *xp = xl + b * K + c * 512 + lane * 8;
+        f32x4 xa = *(const f32x4 *)xp, xb = *(const f32x4 *)(xp + 4);
+#pragma unroll
+        for (int r = 0; r < RPW; r++) acc[r][b] = dot8(w[r][c], xa, xb, acc[r][b]);
       }
-      *(f32x4 *)(xl + i) = v;
-    }
-    __syncthreads();
-    if (active) {
-      u32x4 w[RPW][NCH];
-#pragma unroll
-      for (int r = 0; r < RPW; r++) {
-        const uint16_t *rowp;
-        if (EPI == EPI_SWIGLU)
-          rowp = ((r & 1) ? a.W2 : a.W) + (size_t)(unit0 + (r >> 1)) * K;
-        else
-          rowp = a.W + (size_t)min(unit0 + r, a.M - 1) * K;
-#pragma unroll
-        for (int c = 0; c < NCH; c++) w[r][c] = ldw(rowp + kt + c * 512 + lane * 8);
-      }
-#pragma unroll
-      for (int c = 0; c < NCH; c++)
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-          const float *xp = xl + b * KT + c * 512 + lane * 8;
-          f32x4 xa = *(const f32x4 *)xp, xb = *(const f32x4 *)(xp + 4);
-#pragma unroll
-          for (int r = 0; r < RPW; r++) acc[r][b] = dot8(w[r][c], xa, xb, acc[r][b]);
-        }
-    }
   }
   if (!active) return;
 
@@ -600,6 +614,8 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, flo
   float2 o[ATTN_SPLITS];
 #pragma unroll
   for (int s = 0; s < ATTN_SPLITS; s++) o[s] = *(const float2 *)(hp + s * (HD + 2) + lane * 2);
+  // keep every load ahead of the first use (one memory round trip)
+  __builtin_amdgcn_sched_barrier(0);
   const float ms = lane < ATTN_SPLITS ? mv : -INFINITY;
   const float M = wave_max(ms);
   const float wgt = lane < ATTN_SPLITS ? expf(ms - M) : 0.f;
@@ -628,10 +644,17 @@ __global__ void multi_codebook_kernel(const uint16_t *table, const uint32_t *sem
                                       const uint32_t *codes, float *out) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= DIM) return;
+  // all 37 row indices, then all 37 row elements, then the ordered sum
+  uint32_t row[NAC + 1];
+  row[0] = sem[0];
+#pragma unroll
+  for (int k = 0; k < NAC; k++) row[k + 1] = 8194u + k * 23u + codes[k];
+  uint16_t v[NAC + 1];
+#pragma unroll
+  for (int k = 0; k <= NAC; k++) v[k] = table[(size_t)row[k] * DIM + i];
   float s = 0.f;
-  s += h2f(table[(size_t)sem[0] * DIM + i]);
-  for (int k = 0; k < NAC; k++)
-    s += h2f(table[(size_t)(8194u + k * 23u + codes[k]) * DIM + i]);
+#pragma unroll
+  for (int k = 0; k <= NAC; k++) s += h2f(v[k]);
   out[i] = s;
 }
 
@@ -641,8 +664,16 @@ __global__ __launch_bounds__(1024) void final_norm_kernel(const float *x, const 
                                                           float eps, float *normed, int *pos) {
   __shared__ float red[16];
   const int tid = threadIdx.x;
+  static_assert(DIM % 1024 == 0, "threads tile DIM");
+  float xv[DIM / 1024], gv[DIM / 1024];
+#pragma unroll
+  for (int j = 0; j < DIM / 1024; j++) {  // the gains load with x, not after the reduction
+    xv[j] = x[tid + j * 1024];
+    gv[j] = h2f(w[tid + j * 1024]);
+  }
   float s = 0.f;
-  for (int i = tid; i < DIM; i += 1024) s += x[i] * x[i];
+#pragma unroll
+  for (int j = 0; j < DIM / 1024; j++) s += xv[j] * xv[j];
   s = wave_sum(s);
   if ((tid & 63) == 0) red[tid >> 6] = s;
   __syncthreads();
@@ -650,7 +681,8 @@ __global__ __launch_bounds__(1024) void final_norm_kernel(const float *x, const 
 #pragma unroll
   for (int k = 0; k < 16; k++) tot += red[k];
   const float rms = 1.0f / sqrtf(tot / (float)DIM + eps);
-  for (int i = tid; i < DIM; i += 1024) normed[i] = x[i] * rms * h2f(w[i]);
+#pragma unroll
+  for (int j = 0; j < DIM / 1024; j++) normed[tid + j * 1024] = xv[j] * rms * gv[j];
   if (pos != nullptr && tid == 0) *pos += 1;
 }
 
@@ -1179,6 +1211,14 @@ struct FmStepArgs {
 __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
   __shared__ float xs[NAC];
   const int t = threadIdx.x;
+  const int row = blockIdx.x * 256 + t;  // grid covers DIM exactly
+  // this row's input-projection weights, time/llm projections and gain do
+  // not depend on x_s: issued first, they arrive while x_s is formed
+  uint2 wr[NAC / 4];
+#pragma unroll
+  for (int j = 0; j < NAC / 4; j++) wr[j] = ((const uint2 *)(a.w_in + (size_t)row * NAC))[j];
+  const float tp = a.tproj[row], lp = a.llm[row];
+  const float g = h2f(a.gn[row]);
   if (t < NAC) {
     float x;
     if (a.step == 0) {
@@ -1191,14 +1231,16 @@ __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
     if (blockIdx.x == 0) a.xh[a.step * NAC + t] = x;
   }
   __syncthreads();
-  const int row = blockIdx.x * 256 + t;  // grid covers DIM exactly
-  const uint16_t *w = a.w_in + (size_t)row * NAC;
   float acc = 0.f;
 #pragma unroll
-  for (int k = 0; k < NAC; k++) acc = fmaf(h2f(w[k]), xs[k], acc);
-  const float tp = a.tproj[row], lp = a.llm[row];
+  for (int j = 0; j < NAC / 4; j++) {
+    const h2 w01 = __builtin_bit_cast(h2, wr[j].x), w23 = __builtin_bit_cast(h2, wr[j].y);
+    acc = fmaf((float)w01.x, xs[4 * j], acc);
+    acc = fmaf((float)w01.y, xs[4 * j + 1], acc);
+    acc = fmaf((float)w23.x, xs[4 * j + 2], acc);
+    acc = fmaf((float)w23.y, xs[4 * j + 3], acc);
+  }
   const float y[FMV] = {acc, tp, lp, acc, tp, 0.f};
-  const float g = h2f(a.gn[row]);
   __shared__ float red[4][FMV];
 #pragma unroll
   for (int v = 0; v < FMV; v++) {
