@@ -235,6 +235,50 @@ void launch_gemm6(hipStream_t st, const Gemm6Args &a, int rows) {
   hipLaunchKernelGGL((gemm6_kernel<EPI, K, RG, KS, P>), dim3(rows / (FTR * RG)), dim3(RG * KS * 64),
                      0, st, a);
 }
+// Launch shapes of the four FM GEMMs <RG, KS, P>, picked on the whole frame
+// loop.  A build with -DVX_FM_SWEEP selects each from a candidate list by
+// the environment (VX_FM_QKV, VX_FM_O, VX_FM_GATEUP, VX_FM_DOWN = index).
+#ifdef VX_FM_SWEEP
+typedef void (*Gemm6Launch)(hipStream_t, const Gemm6Args &, int);
+static int fm_sweep_pick(const char *name, int n) {
+  const char *v = getenv(name);
+  const int i = v ? atoi(v) : 0;
+  return i < 0 || i >= n ? 0 : i;
+}
+#define FM_PICK(list, name) list[fm_sweep_pick(name, (int)(sizeof(list) / sizeof(list[0])))]
+static const Gemm6Launch kFmQkv[] = {
+    launch_gemm6<EPI_QKV, DIM, 1, 8, 4>,  launch_gemm6<EPI_QKV, DIM, 1, 8, 6>,
+    launch_gemm6<EPI_QKV, DIM, 1, 8, 12>, launch_gemm6<EPI_QKV, DIM, 1, 4, 8>,
+    launch_gemm6<EPI_QKV, DIM, 1, 4, 12>, launch_gemm6<EPI_QKV, DIM, 1, 6, 8>,
+    launch_gemm6<EPI_QKV, DIM, 1, 12, 8>, launch_gemm6<EPI_QKV, DIM, 1, 16, 6>,
+    launch_gemm6<EPI_QKV, DIM, 2, 4, 6>,  launch_gemm6<EPI_QKV, DIM, 2, 8, 4>};
+static const Gemm6Launch kFmO[] = {
+    launch_gemm6<EPI_RESID, QD, 1, 16, 4>, launch_gemm6<EPI_RESID, QD, 1, 16, 8>,
+    launch_gemm6<EPI_RESID, QD, 1, 8, 8>,  launch_gemm6<EPI_RESID, QD, 1, 8, 16>,
+    launch_gemm6<EPI_RESID, QD, 2, 8, 8>,  launch_gemm6<EPI_RESID, QD, 1, 4, 16>,
+    launch_gemm6<EPI_RESID, QD, 1, 16, 2>, launch_gemm6<EPI_RESID, QD, 2, 4, 16>};
+static const Gemm6Launch kFmGateUp[] = {
+    launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 16>, launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 12>,
+    launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 8>,  launch_gemm6<EPI_SWIGLU, DIM, 1, 2, 16>,
+    launch_gemm6<EPI_SWIGLU, DIM, 1, 4, 8>,  launch_gemm6<EPI_SWIGLU, DIM, 1, 4, 12>,
+    launch_gemm6<EPI_SWIGLU, DIM, 1, 8, 12>, launch_gemm6<EPI_SWIGLU, DIM, 1, 8, 6>,
+    launch_gemm6<EPI_SWIGLU, DIM, 2, 1, 16>};
+static const Gemm6Launch kFmDown[] = {
+    launch_gemm6<EPI_RESID, HID, 1, 12, 12>, launch_gemm6<EPI_RESID, HID, 1, 12, 24>,
+    launch_gemm6<EPI_RESID, HID, 1, 12, 8>,  launch_gemm6<EPI_RESID, HID, 1, 8, 12>,
+    launch_gemm6<EPI_RESID, HID, 1, 16, 9>,  launch_gemm6<EPI_RESID, HID, 1, 16, 18>,
+    launch_gemm6<EPI_RESID, HID, 1, 6, 16>,  launch_gemm6<EPI_RESID, HID, 1, 6, 24>,
+    launch_gemm6<EPI_RESID, HID, 1, 9, 16>,  launch_gemm6<EPI_RESID, HID, 1, 4, 24>};
+#define FM_GEMM_QKV FM_PICK(kFmQkv, "VX_FM_QKV")
+#define FM_GEMM_O FM_PICK(kFmO, "VX_FM_O")
+#define FM_GEMM_GATEUP FM_PICK(kFmGateUp, "VX_FM_GATEUP")
+#define FM_GEMM_DOWN FM_PICK(kFmDown, "VX_FM_DOWN")
+#else
+#define FM_GEMM_QKV (launch_gemm6<EPI_QKV, DIM, 1, 8, 4>)
+#define FM_GEMM_O (launch_gemm6<EPI_RESID, QD, 1, 16, 4>)
+#define FM_GEMM_GATEUP (launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 16>)
+#define FM_GEMM_DOWN (launch_gemm6<EPI_RESID, HID, 1, 12, 12>)
+#endif
 // 12-row tiles divide every FM matrix into a multiple of 256 tiles
 static_assert(QKV_ROWS % (256 * FTR) == 0 && DIM % (256 * FTR) == 0 && HID % (256 * FTR) == 0 &&
                   DIM / FTR <= SSQ_MAX && DIM % 256 == 0,
@@ -375,7 +419,7 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
         a.out = e->fm_q;
         a.out_k = e->fm_k;
         a.out_v = e->fm_v;
-        launch_gemm6<EPI_QKV, DIM, 1, 8, 4>(st, a, QKV_ROWS);
+        FM_GEMM_QKV(st, a, QKV_ROWS);
       }
       hipLaunchKernelGGL(fm_attn_kernel, dim3(NH, 2), dim3(64), 0, st, e->fm_q, e->fm_k, e->fm_v,
                          e->fm_attn, e->fm_b_o);
@@ -388,7 +432,7 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
         a.Bn = e->fm_b_ffn;
         a.gn = W.ffn_norm;
         a.ssq_out = e->fm_ssq_ffn;
-        launch_gemm6<EPI_RESID, QD, 1, 16, 4>(st, a, DIM);
+        FM_GEMM_O(st, a, DIM);
       }
       {  // RMSNorm + gate/up + SwiGLU; hands the activation to down
         Gemm6Args a{};
@@ -401,7 +445,7 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
         a.out = e->fm_act;
         a.os = HID;
         a.Bn = e->fm_b_act;
-        launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 16>(st, a, HID);
+        FM_GEMM_GATEUP(st, a, HID);
       }
       {  // down + residual; hands norm(x) * next attention gains to the next layer
         Gemm6Args a{};
@@ -414,7 +458,7 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
           a.gn = e->FL[l + 1].attn_norm;
           a.ssq_out = e->fm_ssq_attn;
         }
-        launch_gemm6<EPI_RESID, HID, 1, 12, 12>(st, a, DIM);
+        FM_GEMM_DOWN(st, a, DIM);
         nssq_attn = DIM / FTR;
       }
     }
