@@ -881,6 +881,17 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
 #pragma unroll
     for (int v = 0; v < FMV; v++) sv[v] = *(const f32x4 *)(a.ssq + v * SSQ_MAX + lane * 4);
   }
+  // The epilogue's own operands (EPI_RESID: the residual values; the next
+  // GEMM's norm gains) are loaded here too, so the wave that finishes the
+  // block waits on no memory after its last MFMA.  Lanes of the dropped D
+  // rows 12-15 read the tile's first rows instead.
+  const int ev = n < FMV ? n : 0, er = row0 + (drow ? 4 * (lane >> 4) : 0);
+  f32x4 eres = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint2 egn = uint2{0u, 0u};
+  if (kp == 0) {
+    if (EPI == EPI_RESID) eres = *(const f32x4 *)(a.out + (size_t)ev * a.os + er);
+    if (a.Bn && a.gn) egn = *(const uint2 *)(a.gn + er);
+  }
   u32x4 wb[P][TL];
   h8 bb[P];
   auto load = [&](int i, int d) {
@@ -933,7 +944,7 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
   for (int t = 0; t < TL; t++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[t][j] += __shfl(acc[t][j], lane + FMV, 64);
-  const int v = n < FMV ? n : 0, r = row0 + 4 * (lane >> 4);
+  const int v = ev, r = row0 + 4 * (lane >> 4);
   float rv = rs[0];
 #pragma unroll
   for (int u = 1; u < FMV; u++) rv = v == u ? rs[u] : rv;
@@ -946,9 +957,8 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
       for (int j = 0; j < 4; j++) y[j] = (y[j] / (1.0f + expf(-y[j]))) * u[j];
       *(f32x4 *)(a.out + (size_t)v * a.os + r) = y;
     } else if (EPI == EPI_RESID) {
-      f32x4 *o = (f32x4 *)(a.out + (size_t)v * a.os + r);
-      y = y + *o;
-      *o = y;
+      y = y + eres;
+      *(f32x4 *)(a.out + (size_t)v * a.os + r) = y;
     } else if (EPI == EPI_QKV) {
       if (r < QD)
         *(f32x4 *)(a.out + (size_t)v * QD + r) = y;
@@ -966,9 +976,13 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
     s2 += __shfl_xor(s2, 32, 64);
     if (live) {
       f32x4 z = y;
-      if (a.gn)
-#pragma unroll
-        for (int j = 0; j < 4; j++) z[j] *= h2f(a.gn[r + j]);
+      if (a.gn) {
+        const h2 g01 = __builtin_bit_cast(h2, egn.x), g23 = __builtin_bit_cast(h2, egn.y);
+        z[0] *= (float)g01.x;
+        z[1] *= (float)g01.y;
+        z[2] *= (float)g23.x;
+        z[3] *= (float)g23.y;
+      }
       bpack_put4(a.Bn, v, r, z);
       if (a.ssq_out && lane < 16) a.ssq_out[v * SSQ_MAX + tile] = s2;
     }
