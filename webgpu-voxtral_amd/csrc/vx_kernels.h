@@ -696,7 +696,25 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *x, int n, int 
   const int t = threadIdx.x;
   float best = -1e30f;
   uint32_t idx = 0;
-  for (int i = t; i < n; i += 256) {
+  // thread t visits i = t, t+256, ... in order (strict >: the first maximum
+  // wins), loading 16 elements per round trip
+  constexpr int AB = 16;
+  int i = t;
+  for (; i + (AB - 1) * 256 < n; i += AB * 256) {
+    float v[AB];
+#pragma unroll
+    for (int b = 0; b < AB; b++) v[b] = x[i + b * 256];
+#pragma unroll
+    for (int b = 0; b < AB; b++) {
+      const int j = i + b * 256;
+      const float w = mask_valid > 0 && (j == 0 || j >= mask_valid) ? -INFINITY : v[b];
+      if (w > best) {
+        best = w;
+        idx = (uint32_t)j;
+      }
+    }
+  }
+  for (; i < n; i += 256) {
     float v = x[i];
     if (mask_valid > 0 && (i == 0 || i >= mask_valid)) v = -INFINITY;
     if (v > best) {
