@@ -268,4 +268,196 @@ __global__ __launch_bounds__(256) void pf_attn_kernel(const float *Q, const void
   *(hh2 *)bl = hh2{l0, l1};
 }
 
+// ------------------------------------------------ causal attention on MFMA
+// The same result as pf_attn_kernel<float> (attnScore + softmax + attnValue
+// per prompt token over keys 0..pos0+t, src/shaders.ts:306-447) with the
+// products on the matrix cores.  Block = (16-token tile, KV head), wave w =
+// query head 4*kv_head + w; the tile's K and V rows (f32 cache) are staged
+// through LDS 32 keys at a time, V transposed, and shared by the 4 waves.
+// Per 32-key tile and wave, in the transposed form (the token is the MFMA
+// column, so every lane holds one token's values):
+//   S^T[16 keys][16 tokens] = K[16][128] . Q^T[128][16]     16x16x32 f16
+//   O^T[16 dims][16 tokens] += V^T[16][16 keys] . P^T[16 keys][16]   16x16x16 f16
+// The D layout of S^T (lane l: keys 4(l/16)..+3 of token l%16) is exactly
+// the B operand of the 16x16x16 product, so P needs no shuffle; the online
+// softmax rescale of O^T is per lane.  Every f32 operand is split into f16
+// hi + lo and a product is hi.hi + hi.lo + lo.hi, about 2^-21 relative, as
+// in the prefill GEMMs.  Output: hi/lo rows of the O projection's B (rows
+// t and nt + t), zero for t >= n.
+typedef _Float16 hf4 __attribute__((ext_vector_type(4)));
+constexpr int PFA_T = 16;        // tokens per block
+constexpr int PFA_K = 32;        // keys per staged tile
+constexpr int PFA_KW = HD + 4;   // LDS row of K (floats)
+constexpr int PFA_VW = PFA_K + 4;  // LDS row of V^T (floats)
+
+// x = hi + lo in f16 with hi and the remainder from one conversion: hi
+// rounds toward zero (v_cvt_pkrtz_f16_f32, two values per instruction), and
+// lo = f16(x - hi) is formed from that same hi, so hi + lo equals x to about
+// 2^-21 whatever rounding hi took.  (Converting hi twice, once packed for the
+// operand and once scalar for the remainder, let the generated code pair a lo
+// with a hi other than the operand's: sums one f16 ulp off in places.)
+template <int N, typename V>
+__device__ __forceinline__ void split_n(const float (&x)[N], V &hi, V &lo) {
+#pragma unroll
+  for (int j = 0; j < N; j += 2) {
+    const auto h = __builtin_amdgcn_cvt_pkrtz(x[j], x[j + 1]);
+    const auto l = __builtin_amdgcn_cvt_pkrtz(x[j] - (float)h[0], x[j + 1] - (float)h[1]);
+    hi[j] = h[0];
+    hi[j + 1] = h[1];
+    lo[j] = l[0];
+    lo[j + 1] = l[1];
+  }
+}
+__device__ __forceinline__ void split8(const f32x4 a, const f32x4 b, h8 &hi, h8 &lo) {
+  const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  split_n<8>(x, hi, lo);
+}
+__device__ __forceinline__ void split4(const f32x4 a, hf4 &hi, hf4 &lo) {
+  const float x[4] = {a[0], a[1], a[2], a[3]};
+  split_n<4>(x, hi, lo);
+}
+
+__global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const float *kc, const float *vc,
+                                                           int max_seq, int pos0, int n, int nt, h8 *B) {
+  const int t0 = blockIdx.x * PFA_T, kvh = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = kvh * (NH / NKV) + wave;
+  const int col = lane & 15, grp = lane >> 4;  // MFMA column (token) and row group
+  const int t = t0 + col;                      // this lane's token
+  __shared__ __attribute__((aligned(16))) float ks[PFA_K * PFA_KW];
+  __shared__ __attribute__((aligned(16))) float vt[HD * PFA_VW];
+  if (t0 >= n) {  // padding columns of the GEMM: zero hi and lo
+    _Float16 *p = (_Float16 *)B;
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) {
+      const size_t c = (size_t)h * HD + dt * 16 + 4 * grp;
+      *(hf4 *)(p + (size_t)t * QD + c) = hf4{0, 0, 0, 0};
+      *(hf4 *)(p + (size_t)(nt + t) * QD + c) = hf4{0, 0, 0, 0};
+    }
+    return;
+  }
+  const float *Kb = kc + (size_t)kvh * max_seq * HD;
+  const float *Vb = vc + (size_t)kvh * max_seq * HD;
+  const int last = pos0 + min(t, n - 1);         // last key of this lane's token
+  const int kend = pos0 + min(t0 + PFA_T, n);    // keys of the tile: [0, kend)
+  const int ntile = (kend + PFA_K - 1) / PFA_K;
+
+  // staging: thread i holds 4 float4 of K and of V: row (i / 32) + 8j, dims 4*(i % 32)
+  const int srow = tid >> 5, sdim = (tid & 31) * 4;
+  f32x4 kr[4], vr[4];
+  auto load_tile = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int key = min(kb + srow + 8 * j, kend - 1);  // rows past the keys re-read the last
+      kr[j] = *(const f32x4 *)(Kb + (size_t)key * HD + sdim);
+      vr[j] = *(const f32x4 *)(Vb + (size_t)key * HD + sdim);
+    }
+  };
+  load_tile(0);
+
+  // Q^T operand of S^T (token t, dims 32c + 8grp..+8), hi and lo; padding tokens zero
+  h8 qh[HD / 32], ql[HD / 32];
+  {
+    const float *qp = Q + (size_t)min(t, n - 1) * QD + h * HD + 8 * grp;
+#pragma unroll
+    for (int c = 0; c < HD / 32; c++) {
+      f32x4 a = *(const f32x4 *)(qp + 32 * c), b = *(const f32x4 *)(qp + 32 * c + 4);
+      if (t >= n) a = b = f32x4{0.f, 0.f, 0.f, 0.f};
+      split8(a, b, qh[c], ql[c]);
+    }
+  }
+  const float scale = 1.0f / sqrtf((float)HD);
+  float m = -INFINITY, l = 0.f;
+  f32x4 o[HD / 16];
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int it = 0; it < ntile; it++) {
+    const int kb = it * PFA_K;
+    __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int r = srow + 8 * j;
+      *(f32x4 *)(ks + r * PFA_KW + sdim) = kr[j];
+#pragma unroll
+      for (int q = 0; q < 4; q++) vt[(sdim + q) * PFA_VW + r] = vr[j][q];
+    }
+    if (it + 1 < ntile) load_tile(kb + PFA_K);
+    __syncthreads();
+
+    // S^T for keys kb + 16kt + (4grp..+3), token col
+    f32x4 s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+      const float *kp = ks + (16 * kt + col) * PFA_KW + 8 * grp;
+#pragma unroll
+      for (int c = 0; c < HD / 32; c++) {
+        h8 kh, kl;
+        split8(*(const f32x4 *)(kp + 32 * c), *(const f32x4 *)(kp + 32 * c + 4), kh, kl);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[c], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], acc, 0, 0, 0);
+      }
+      s[kt] = acc;
+    }
+    // online softmax of token col over this tile's keys (8 per lane, 4 lanes per token)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int key = kb + 16 * kt + 4 * grp + i;
+        const float v = key <= last ? s[kt][i] * scale : -INFINITY;
+        s[kt][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(m, mx);  // finite: key 0 <= last is in the first tile
+    const float corr = expf(m - mnew);
+    float ps = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float e = s[kt][i] == -INFINITY ? 0.f : expf(s[kt][i] - mnew);
+        s[kt][i] = e;
+        ps += e;
+      }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * corr + ps;
+    m = mnew;
+    // O^T += V^T . P^T
+    hf4 ph[2], pl[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) split4(s[kt], ph[kt], pl[kt]);
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) {
+      f32x4 acc = o[dt] * corr;
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        hf4 vh, vl;
+        split4(*(const f32x4 *)(vt + (16 * dt + col) * PFA_VW + 16 * kt + 4 * grp), vh, vl);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, ph[kt], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph[kt], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, pl[kt], acc, 0, 0, 0);
+      }
+      o[dt] = acc;
+    }
+  }
+  // out[t][dims] = O^T / l, as hi and lo f16 rows of B (zero past n)
+  _Float16 *p = (_Float16 *)B;
+  const float inv = 1.0f / l;
+#pragma unroll
+  for (int dt = 0; dt < HD / 16; dt++) {
+    hf4 hi = hf4{0, 0, 0, 0}, lo = hf4{0, 0, 0, 0};
+    if (t < n) split4(o[dt] * inv, hi, lo);
+    const size_t c = (size_t)h * HD + dt * 16 + 4 * grp;
+    *(hf4 *)(p + (size_t)t * QD + c) = hi;
+    *(hf4 *)(p + (size_t)(nt + t) * QD + c) = lo;
+  }
+}
+
 }  // namespace vx
