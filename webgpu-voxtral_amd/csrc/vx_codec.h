@@ -47,11 +47,7 @@ __device__ __forceinline__ float cx_val(const float *C, int ldc, int nc, int t, 
 // k group kb (8 halves) of columns t (hi) and nt + t (lo); kg = K / 8
 __device__ __forceinline__ void cx_put(h8 *B, int nc, int kg, int kb, int t, const float (&y)[8]) {
   h8 hi, lo;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    hi[e] = (_Float16)y[e];
-    lo[e] = (_Float16)(y[e] - (float)hi[e]);
-  }
+  split_n<8>(y, hi, lo);
   B[(size_t)t * kg + kb] = hi;
   B[(size_t)((nc >> 1) + t) * kg + kb] = lo;
 }

@@ -75,9 +75,38 @@ __device__ __forceinline__ float h2f(uint16_t b) {
 __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, RNE
 }
+// x = hi + lo in f16 for two values: hi = f16(x) rounded toward zero, from
+// one v_cvt_pkrtz_f16_f32, and lo = f16(x - hi) rounded to nearest even from
+// that same hi, so |x - hi - lo| <= 2^-21 |x| for normal hi (f16 subnormals
+// are kept).  The sum is only that close when lo is formed from the very hi
+// that is stored.  Written as plain casts, the compiler converts hi twice
+// (packed for the stored operand, scalar for the remainder), and the pairing
+// then rests on both conversions being generated right; this compiler has
+// been seen to emit the packed one with its second source replaced by the
+// first.  Inline asm is no way out: the hazard recognizer does not count an
+// asm statement as a vector-ALU write, so an MFMA that reads its result gets
+// no wait states and reads the register's old contents.
+__device__ __forceinline__ void split2(float a, float b, h2 &hi, h2 &lo) {
+  const auto h = __builtin_amdgcn_cvt_pkrtz(a, b);
+  hi = h2{(_Float16)h[0], (_Float16)h[1]};
+  lo = h2{(_Float16)(a - (float)h[0]), (_Float16)(b - (float)h[1])};
+}
+// split2 over N values (N even) into f16 vectors of N lanes
+template <int N, typename V>
+__device__ __forceinline__ void split_n(const float (&x)[N], V &hi, V &lo) {
+#pragma unroll
+  for (int j = 0; j < N; j += 2) {
+    h2 h, l;
+    split2(x[j], x[j + 1], h, l);
+    hi[j] = h[0];
+    hi[j + 1] = h[1];
+    lo[j] = l[0];
+    lo[j + 1] = l[1];
+  }
+}
 // IEEE binary16 round-to-nearest-even in integer arithmetic, subnormals
-// included (the hardware conversion flushes f16 subnormals); used where
-// results must be bit-identical to the CPU generator.
+// included; used where results must be bit-identical to the CPU generator
+// whatever the device's float mode.
 __device__ __forceinline__ uint16_t f2h_exact(float f) {
   const uint32_t x = __builtin_bit_cast(uint32_t, f);
   const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
@@ -800,9 +829,11 @@ __global__ void gen_kv_kernel(KVT *cache, int max_seq, int npos, uint64_t seed, 
 //    group l/16; lanes of rows 12-15 load nothing (zeros), so one chunk's
 //    operand is a contiguous 768-byte read;
 //  - B operand: the packed input [k/8][BCOL] of 8-half groups, column v the
-//    hi part f16(y_v) and column FMV+v the lo part f16(y_v - hi): W is exactly
-//    f16, so D[.][v] + D[.][FMV+v] is the f32 dot product up to rounding of
-//    order 2^-22 (f16 subnormals are kept by the conversion).  Columns 12-15
+//    hi part f16(y_v) and column FMV+v the lo part f16(y_v - hi) (split2): W
+//    is exactly f16, so D[.][v] + D[.][FMV+v] is the f32 dot product up to
+//    rounding of order 2^-21 (f16 subnormals are kept by the conversion).
+//    (The fused input kernel rounds hi to nearest, from the product y*g, and
+//    lo from that same hi: order 2^-22.)  Columns 12-15
 //    and rows 12-15 of D are never read.
 // The kernel that produces a GEMM's input writes this packed form in its
 // epilogue, with the next RMSNorm's gains already applied; the RMS scale
@@ -815,20 +846,25 @@ constexpr int FTR = 12;       // rows per FM weight tile
 constexpr int SSQ_MAX = 256;  // partial sums of squares per vector (row tiles of a DIM output)
 
 __device__ __forceinline__ void bpack_put(h8 *B, int v, int k, float y) {
-  const _Float16 hi = (_Float16)y, lo = (_Float16)(y - (float)hi);
+  const _Float16 hi = (_Float16)y, lo = (_Float16)(y - (float)hi);  // one scalar conversion
   _Float16 *p = (_Float16 *)(B + (k >> 3) * BCOL);
   p[v * 8 + (k & 7)] = hi;
   p[(FMV + v) * 8 + (k & 7)] = lo;
+}
+// two consecutive k (k even) of vector v
+__device__ __forceinline__ void bpack_put2(h8 *B, int v, int k, float y0, float y1) {
+  h2 hi, lo;
+  split2(y0, y1, hi, lo);
+  _Float16 *p = (_Float16 *)(B + (k >> 3) * BCOL);
+  *(h2 *)(p + v * 8 + (k & 7)) = hi;
+  *(h2 *)(p + (FMV + v) * 8 + (k & 7)) = lo;
 }
 // four consecutive k (k % 4 == 0) of vector v
 __device__ __forceinline__ void bpack_put4(h8 *B, int v, int k, f32x4 y) {
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   h4 hi, lo;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    hi[j] = (_Float16)y[j];
-    lo[j] = (_Float16)(y[j] - (float)hi[j]);
-  }
+  const float x[4] = {y[0], y[1], y[2], y[3]};
+  split_n<4>(x, hi, lo);
   _Float16 *p = (_Float16 *)(B + (k >> 3) * BCOL);
   *(h4 *)(p + v * 8 + (k & 7)) = hi;
   *(h4 *)(p + (FMV + v) * 8 + (k & 7)) = lo;
@@ -1318,8 +1354,7 @@ __global__ __launch_bounds__(64) void fm_attn_kernel(const float *q, const float
     const float o1 = e0 * vv[0][1] + e1 * vv[1][1] + e2 * vv[2][1];
     out[(size_t)vec * QD + h * HD + lane * 2] = o0;
     out[(size_t)vec * QD + h * HD + lane * 2 + 1] = o1;
-    bpack_put(Bn, vec, h * HD + lane * 2, o0);
-    bpack_put(Bn, vec, h * HD + lane * 2 + 1, o1);
+    bpack_put2(Bn, vec, h * HD + lane * 2, o0, o1);
   }
 }
 

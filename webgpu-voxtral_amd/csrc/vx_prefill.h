@@ -63,13 +63,13 @@ __global__ __launch_bounds__(256) void pf_pack_kernel(const float *X, int K, int
   }
   for (int kb = tid; kb < K / 8; kb += 256) {
     h8 hi, lo;
+    float y[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
       const int k = kb * 8 + e;
-      const float y = t < n ? (NORM ? x[k] * r * h2f(g[k]) : x[k]) : 0.f;
-      hi[e] = (_Float16)y;
-      lo[e] = (_Float16)(y - (float)hi[e]);
+      y[e] = t < n ? (NORM ? x[k] * r * h2f(g[k]) : x[k]) : 0.f;
     }
+    split_n<8>(y, hi, lo);
     B[(size_t)t * (K / 8) + kb] = hi;
     B[(size_t)(nt + t) * (K / 8) + kb] = lo;
   }
@@ -101,11 +101,7 @@ __global__ void pf_qkv_epi_kernel(const float *C, int nt, float *Q, void *kc, vo
 // hi/lo halves of y into B columns t and nt + t at k (8 consecutive k)
 __device__ __forceinline__ void pf_put8(h8 *B, int K, int nt, int t, int kb, const float (&y)[8]) {
   h8 hi, lo;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    hi[e] = (_Float16)y[e];
-    lo[e] = (_Float16)(y[e] - (float)hi[e]);
-  }
+  split_n<8>(y, hi, lo);
   B[(size_t)t * (K / 8) + kb] = hi;
   B[(size_t)(nt + t) * (K / 8) + kb] = lo;
 }
@@ -261,11 +257,10 @@ __global__ __launch_bounds__(256) void pf_attn_kernel(const float *Q, const void
     }
   }
   const float y0 = o0 / l, y1 = o1 / l;
-  const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
-  const _Float16 l0 = (_Float16)(y0 - (float)h0), l1 = (_Float16)(y1 - (float)h1);
-  typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
-  *(hh2 *)bh = hh2{h0, h1};
-  *(hh2 *)bl = hh2{l0, l1};
+  h2 hi, lo;
+  split2(y0, y1, hi, lo);
+  *(h2 *)bh = hi;
+  *(h2 *)bl = lo;
 }
 
 // ------------------------------------------------ causal attention on MFMA
@@ -281,33 +276,17 @@ __global__ __launch_bounds__(256) void pf_attn_kernel(const float *Q, const void
 // The D layout of S^T (lane l: keys 4(l/16)..+3 of token l%16) is exactly
 // the B operand of the 16x16x16 product, so P needs no shuffle; the online
 // softmax rescale of O^T is per lane.  Every f32 operand is split into f16
-// hi + lo and a product is hi.hi + hi.lo + lo.hi, about 2^-21 relative, as
-// in the prefill GEMMs.  Output: hi/lo rows of the O projection's B (rows
-// t and nt + t), zero for t >= n.
+// hi + lo and a product is hi.hi + hi.lo + lo.hi, about 2^-20 relative (the
+// dropped lo.lo term), where the prefill GEMMs, with exact f16 weights, are
+// at the split's 2^-21.  Output: hi/lo
+// rows of the O projection's B (rows t and nt + t), zero for t >= n.
 typedef _Float16 hf4 __attribute__((ext_vector_type(4)));
 constexpr int PFA_T = 16;        // tokens per block
 constexpr int PFA_K = 32;        // keys per staged tile
 constexpr int PFA_KW = HD + 4;   // LDS row of K (floats)
 constexpr int PFA_VW = PFA_K + 4;  // LDS row of V^T (floats)
 
-// x = hi + lo in f16 with hi and the remainder from one conversion: hi
-// rounds toward zero (v_cvt_pkrtz_f16_f32, two values per instruction), and
-// lo = f16(x - hi) is formed from that same hi, so hi + lo equals x to about
-// 2^-21 whatever rounding hi took.  (Converting hi twice, once packed for the
-// operand and once scalar for the remainder, let the generated code pair a lo
-// with a hi other than the operand's: sums one f16 ulp off in places.)
-template <int N, typename V>
-__device__ __forceinline__ void split_n(const float (&x)[N], V &hi, V &lo) {
-#pragma unroll
-  for (int j = 0; j < N; j += 2) {
-    const auto h = __builtin_amdgcn_cvt_pkrtz(x[j], x[j + 1]);
-    const auto l = __builtin_amdgcn_cvt_pkrtz(x[j] - (float)h[0], x[j + 1] - (float)h[1]);
-    hi[j] = h[0];
-    hi[j + 1] = h[1];
-    lo[j] = l[0];
-    lo[j + 1] = l[1];
-  }
-}
+// hi/lo operand halves (split2) of 8 or 4 staged f32 values
 __device__ __forceinline__ void split8(const f32x4 a, const f32x4 b, h8 &hi, h8 &lo) {
   const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   split_n<8>(x, hi, lo);
