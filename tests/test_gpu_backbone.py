@@ -71,6 +71,28 @@ def test_load_tensor_roundtrip_and_errors(pair1):
     assert g.is_ready
 
 
+def test_code_and_position_argument_errors(pair1):
+    """Out-of-range codes and positions are rejected on the host, before any
+    kernel could index past the embedding table or the KV cache (semantic
+    codes of 2^31 and more included: the bound is an unsigned compare)."""
+    import voxtral_amd as V
+    g, _ = pair1
+    for bad in (9088, 2**31, 2**32 - 1):
+        with pytest.raises(V.VoxtralError, match="semantic code"):
+            g.set_semantic_code(bad)
+    g.set_semantic_code(9087)  # the table's last row
+    with pytest.raises(V.VoxtralError, match="acoustic code"):
+        g.set_acoustic_codes(np.full(36, 23, np.uint32))
+    with pytest.raises(V.VoxtralError, match="out of range"):
+        g.position = 1025
+    with pytest.raises(V.VoxtralError, match="out of range"):
+        g.position = -1
+    g.position = 1024
+    with pytest.raises(V.VoxtralError, match="max_seq_len"):
+        g.backbone_step(token=1)
+    g.position = 0
+
+
 def test_single_layer_decode_at_128(pair1):
     g, o = pair1
     x = O.gen_f32(SEED, "input.hidden", 3072)

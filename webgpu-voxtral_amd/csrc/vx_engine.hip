@@ -1232,7 +1232,9 @@ int vx_fm_forward(vx_engine *e, const float *noise, float *sem_logits, uint32_t 
 
 int vx_set_semantic_code(vx_engine *e, uint32_t code) {
   if (!e) return VX_E_INVALID;
-  if ((int)code >= e->cfg.audio_vocab) return fail(e, VX_E_INVALID, "semantic code %u out of range", code);
+  // unsigned compare: a code of 2^31 or more must not pass as a negative int
+  if (code >= (uint32_t)e->cfg.audio_vocab)
+    return fail(e, VX_E_INVALID, "semantic code %u out of range", code);
   hipLaunchKernelGGL(set_u32_kernel, dim3(1), dim3(1), 0, e->st, e->sem_code, code);
   LAUNCHCHK(e);
   return VX_OK;
@@ -1473,7 +1475,7 @@ int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t au
   if (rc) return rc;
   if (n_tokens < 1 || !tokens || audio_count < 0 || (audio_count > 0 && audio_start < 0))
     return fail(e, VX_E_INVALID, "bad prefill arguments");
-  if (e->host_pos + n_tokens > e->max_seq)
+  if ((int64_t)e->host_pos + n_tokens > e->max_seq)
     return fail(e, VX_E_RANGE, "prefill passes max_seq_len %d", e->max_seq);
   for (int i = 0; i < n_tokens; i++)
     if (tokens[i] < 0 || tokens[i] >= e->cfg.vocab_size)
@@ -1808,7 +1810,7 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
   if (rc) return fail(e, VX_E_STATE, "Engine not initialized. Call init() and loadWeights() first.");
   if (n_tokens < 0 || (n_tokens > 0 && !tokens) || max_frames < 0)
     return fail(e, VX_E_INVALID, "bad arguments");
-  if (n_tokens + 1 + (max_frames > 0 ? max_frames - 1 : 0) > e->max_seq)
+  if ((int64_t)n_tokens + 1 + (max_frames > 0 ? max_frames - 1 : 0) > e->max_seq)
     return fail(e, VX_E_RANGE, "prompt + frames exceed max_seq_len %d", e->max_seq);
   vx_generate_options opt;
   vx_generate_options_default(&opt);
