@@ -1999,7 +1999,8 @@ int vx_time_backbone_steps(vx_engine *e, int32_t n, int32_t hold, float *out_ms)
   if (!e || n < 1 || !out_ms) return VX_E_INVALID;
   int rc = check_ready(e);
   if (rc) return rc;
-  if (e->host_pos + (hold ? 1 : n) > e->max_seq) return fail(e, VX_E_RANGE, "steps pass max_seq_len");
+  if ((int64_t)e->host_pos + (hold ? 1 : n) > e->max_seq)
+    return fail(e, VX_E_RANGE, "steps pass max_seq_len");
   HIPCHK(e, hipEventRecord(e->ev0, e->st));
   for (int i = 0; i < n; i++) {
     rc = hold ? run_step_hold(e) : run_step(e);
@@ -2016,7 +2017,7 @@ int vx_time_frames(vx_engine *e, int32_t n, float *out_ms) {
   if (!e || n < 1 || !out_ms) return VX_E_INVALID;
   int rc = check_ready(e);
   if (rc) return rc;
-  if (e->host_pos + n > e->max_seq) return fail(e, VX_E_RANGE, "frames pass max_seq_len");
+  if ((int64_t)e->host_pos + n > e->max_seq) return fail(e, VX_E_RANGE, "frames pass max_seq_len");
   if ((rc = ensure_tproj(e))) return rc;
   if (e->use_graphs && !e->frame_exec && (rc = capture(e, &e->frame_exec, frame_body)))
     return rc;
