@@ -230,7 +230,7 @@ GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, in
 }  // namespace
 
 #ifndef VX_PF_ATTN_MFMA
-#define VX_PF_ATTN_MFMA 1  // prompt attention on the matrix cores (f32 KV cache)
+#define VX_PF_ATTN_MFMA 1  // prompt attention on the matrix cores
 #endif
 
 // FM GEMM launch: `rows` output rows in tiles of FTR, RG tiles per block.
@@ -1436,9 +1436,13 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
     hipLaunchKernelGGL(pf_qkv_epi_kernel, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c, nt,
                        e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
     if (e->kv_f32 && VX_PF_ATTN_MFMA)
-      hipLaunchKernelGGL(pf_attn_mfma_kernel, dim3(nt / PFA_T, NKV), blk, 0, st, e->pf_q,
+      hipLaunchKernelGGL(pf_attn_mfma_kernel<float>, dim3(nt / PFA_T, NKV), blk, 0, st, e->pf_q,
                          (const float *)e->kc(l), (const float *)e->vc(l), e->max_seq, pos0, n, nt,
                          e->pf_b);
+    else if (VX_PF_ATTN_MFMA)
+      hipLaunchKernelGGL(pf_attn_mfma_kernel<uint16_t>, dim3(nt / PFA_T, NKV), blk, 0, st, e->pf_q,
+                         (const uint16_t *)e->kc(l), (const uint16_t *)e->vc(l), e->max_seq, pos0,
+                         n, nt, e->pf_b);
     else if (e->kv_f32)
       hipLaunchKernelGGL(pf_attn_kernel<float>, dim3(nt, NKV), blk, 0, st, e->pf_q, e->kc(l),
                          e->vc(l), e->max_seq, pos0, n, nt, e->pf_b);

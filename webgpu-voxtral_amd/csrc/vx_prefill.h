@@ -296,7 +296,21 @@ __device__ __forceinline__ void split4(const f32x4 a, hf4 &hi, hf4 &lo) {
   split_n<4>(x, hi, lo);
 }
 
-__global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const float *kc, const float *vc,
+// 4 consecutive K/V values as held between load and staging: f32 as loaded,
+// f16 as raw halves (widened only when staged, so the prefetch's wait stays
+// at the staging point)
+__device__ __forceinline__ f32x4 pfa_ld4(const float *p) { return *(const f32x4 *)p; }
+__device__ __forceinline__ uint2 pfa_ld4(const uint16_t *p) { return *(const uint2 *)p; }
+__device__ __forceinline__ f32x4 pfa_widen(f32x4 v) { return v; }
+__device__ __forceinline__ f32x4 pfa_widen(uint2 v) {
+  const h2 a = __builtin_bit_cast(h2, v.x), b = __builtin_bit_cast(h2, v.y);
+  return f32x4{(float)a.x, (float)a.y, (float)b.x, (float)b.y};
+}
+
+// KVT = float (f32 cache) or uint16_t (f16 cache: widened exactly to f32 on
+// staging, so its lo halves are zero and the products are exact)
+template <typename KVT>
+__global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const KVT *kc, const KVT *vc,
                                                            int max_seq, int pos0, int n, int nt, h8 *B) {
   const int t0 = blockIdx.x * PFA_T, kvh = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -315,21 +329,21 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const
     }
     return;
   }
-  const float *Kb = kc + (size_t)kvh * max_seq * HD;
-  const float *Vb = vc + (size_t)kvh * max_seq * HD;
+  const KVT *Kb = kc + (size_t)kvh * max_seq * HD;
+  const KVT *Vb = vc + (size_t)kvh * max_seq * HD;
   const int last = pos0 + min(t, n - 1);         // last key of this lane's token
   const int kend = pos0 + min(t0 + PFA_T, n);    // keys of the tile: [0, kend)
   const int ntile = (kend + PFA_K - 1) / PFA_K;
 
-  // staging: thread i holds 4 float4 of K and of V: row (i / 32) + 8j, dims 4*(i % 32)
+  // staging: thread i holds 4 x 4 values of K and of V: row (i / 32) + 8j, dims 4*(i % 32)
   const int srow = tid >> 5, sdim = (tid & 31) * 4;
-  f32x4 kr[4], vr[4];
+  decltype(pfa_ld4(Kb)) kr[4], vr[4];
   auto load_tile = [&](int kb) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int key = min(kb + srow + 8 * j, kend - 1);  // rows past the keys re-read the last
-      kr[j] = *(const f32x4 *)(Kb + (size_t)key * HD + sdim);
-      vr[j] = *(const f32x4 *)(Vb + (size_t)key * HD + sdim);
+      kr[j] = pfa_ld4(Kb + (size_t)key * HD + sdim);
+      vr[j] = pfa_ld4(Vb + (size_t)key * HD + sdim);
     }
   };
   load_tile(0);
@@ -357,9 +371,10 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int r = srow + 8 * j;
-      *(f32x4 *)(ks + r * PFA_KW + sdim) = kr[j];
+      const f32x4 kw = pfa_widen(kr[j]), vw = pfa_widen(vr[j]);
+      *(f32x4 *)(ks + r * PFA_KW + sdim) = kw;
 #pragma unroll
-      for (int q = 0; q < 4; q++) vt[(sdim + q) * PFA_VW + r] = vr[j][q];
+      for (int q = 0; q < 4; q++) vt[(sdim + q) * PFA_VW + r] = vw[q];
     }
     if (it + 1 < ntile) load_tile(kb + PFA_K);
     __syncthreads();
