@@ -95,6 +95,8 @@ def lib():
             "vxo_backbone_step_codes": (None, [c_vp]),
             "vxo_fm_forward": (None, [c_vp, F32]),
             "vxo_fm_forward_batched": (None, [c_vp, F32]),
+            "vxo_generate": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_u64, c_int,
+                                     c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp]),
             # codec decoder (vx_oracle_codec.c)
             "vxo_normalize_codebook": (None, [U16, U16, U16, c_int, c_int, c_float]),
             "vxo_vq_lookup": (None, [U32, U16, F32, c_int, c_int, c_int]),
@@ -352,6 +354,49 @@ class OracleEngine:
     def fm_forward(self, noise, batched=False):
         noise = np.ascontiguousarray(noise, np.float32)
         (lib().vxo_fm_forward_batched if batched else lib().vxo_fm_forward)(self._h, noise)
+
+    def generate(self, tokens, audio_token_start, audio_token_count, voice_embeddings,
+                 max_frames, noise_seed=0, ignore_eos=False, forced_semantic=None,
+                 forced_acoustic=None, want_normed=False, want_logits=False):
+        """generate() up to the codec decode (src/engine.ts:2416-2585): greedy
+        masked semantic codes, FM noise from the engine's seeded fm.noise
+        stream.  forced_semantic [n] / forced_acoustic [n][36]: the state
+        each of the first n frames hands to the next (teacher forcing).
+        Returns a dict of the per-frame outputs for every frame computed,
+        including an EOS frame (framesGenerated = "frames")."""
+        c = self.cfg
+        toks = np.ascontiguousarray(tokens, np.int32)
+        voice = None
+        if voice_embeddings is not None:
+            voice = np.ascontiguousarray(voice_embeddings, np.float32).ravel()
+            if voice.size < audio_token_count * c.dim:
+                raise ValueError("voice embeddings shorter than audio_token_count rows")
+        n = max_frames
+        sem = np.zeros(n, np.uint32)
+        ac = np.zeros((n, c.n_acoustic_out), np.uint32)
+        xt = np.zeros((n, c.n_acoustic_out), np.float32)
+        normed = np.zeros((n, c.dim), np.float32) if want_normed else None
+        logits = np.zeros((n, c.semantic_vocab), np.float32) if want_logits else None
+        fs = fa = None
+        nf = 0
+        if forced_semantic is not None:
+            fs = np.ascontiguousarray(forced_semantic, np.uint32)
+            fa = np.ascontiguousarray(forced_acoustic, np.uint32).reshape(-1, c.n_acoustic_out)
+            nf = min(fs.size, fa.shape[0])
+        ptr = lambda a: a.ctypes.data if a is not None else None
+        frames = lib().vxo_generate(self._h, ptr(toks), toks.size, int(audio_token_start),
+                                    int(audio_token_count), ptr(voice), n, noise_seed,
+                                    int(bool(ignore_eos)), ptr(fs), ptr(fa), nf, ptr(sem),
+                                    ptr(ac), ptr(xt), ptr(normed), ptr(logits))
+        if frames < 0:
+            raise ValueError("prompt + frames exceed max_seq")
+        m = min(frames + 1, n)  # the EOS frame's outputs too, when computed
+        out = {"frames": frames, "semantic": sem[:m], "acoustic": ac[:m], "x_t": xt[:m]}
+        if want_normed:
+            out["normed"] = normed[:m]
+        if want_logits:
+            out["logits"] = logits[:m]
+        return out
 
 
 # ---------------------------------------------------------- codec decoder

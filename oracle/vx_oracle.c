@@ -1035,3 +1035,75 @@ void vxo_fm_forward_batched(vxo_engine *e, const float *noise) {
   free(seq);
   free(vel);
 }
+
+/* generate(), src/engine.ts:2416-2585, up to the codec decode.
+ *   prefill: one backboneStep per prompt token, the voice rows replacing the
+ *     embeddings of positions [audio_start, audio_start + audio_count)
+ *     (:2453-2472);
+ *   AUDIO kick: token 24 through the text embedding (:2478-2487);
+ *   frame 0: fmForward only; frame f > 0: multi-codebook embedding of the
+ *     previous frame's codes as a precomputed row, then a backboneStep
+ *     (:2499-2542), then fmForward;
+ *   semantic code: logits with index 0 and indices >= 8194 masked
+ *     (:2556-2563), then the 256-lane tree argmax (greedy, in place of
+ *     sampleTopP :2565, whose Math.random nothing can reproduce);
+ *   EOS on a semantic code <= 1 (:2568-2570).
+ * The FM noise of frame f is x_0[i] = vxo_normal(noise_seed, stream("fm.noise"),
+ * 36 f + i) (the debugNoise path, :1266).  Teacher forcing: with forced_sem
+ * and forced_ac (n_forced frames), frame f's own codes are reported but the
+ * state the next frame embeds is forced_*[f], and EOS is not taken for
+ * f < n_forced.  Returns the number of frames with a non-EOS code
+ * (framesGenerated); per frame f < that count (and for the EOS frame, which
+ * is reported at index `return value` when max_frames allows) the optional
+ * outputs receive: sem_out[f], ac_out[36 f..], x_out[36 f..] (x_t after the
+ * last Euler update), normed_out[dim f..] (the backbone's final norm that
+ * fed the FM), logits_out[8320 f..] (unmasked semantic logits). */
+int vxo_generate(vxo_engine *e, const int32_t *tokens, int n_tokens, int audio_start,
+                 int audio_count, const float *voice, int max_frames, uint64_t noise_seed,
+                 int ignore_eos, const uint32_t *forced_sem, const uint32_t *forced_ac,
+                 int n_forced, uint32_t *sem_out, uint32_t *ac_out, float *x_out,
+                 float *normed_out, float *logits_out) {
+  const vxo_config *c = &e->c;
+  const int d = c->dim, na = c->n_acoustic_out, sv = c->semantic_vocab;
+  const int valid = 8194; /* 8192 codebook entries + 2 specials, :2561 */
+  if (n_tokens < 0 || max_frames < 0 || (long)n_tokens + max_frames + 1 > e->max_seq) return -1;
+  vxo_reset(e);
+  for (int i = 0; i < n_tokens; i++) {
+    if (voice && audio_count > 0 && i >= audio_start && i < audio_start + audio_count)
+      vxo_backbone_step(e, tokens[i], 2, voice + (size_t)(i - audio_start) * d, 0);
+    else
+      vxo_backbone_step(e, tokens[i], 0, NULL, 0);
+  }
+  vxo_backbone_step(e, 24, 0, NULL, 0);
+  const uint64_t stream = vxo_name_stream("fm.noise");
+  float *noise = falloc((size_t)na), *masked = falloc((size_t)sv);
+  int frames = 0;
+  for (int f = 0; f < max_frames; f++) {
+    if (f > 0) vxo_backbone_step_codes(e);
+    for (int i = 0; i < na; i++) noise[i] = vxo_normal(noise_seed, stream, (uint64_t)f * na + i);
+    vxo_fm_forward_batched(e, noise);
+    memcpy(masked, e->semantic_logits, (size_t)sv * sizeof(float));
+    masked[0] = -INFINITY;
+    for (int i = valid; i < sv; i++) masked[i] = -INFINITY;
+    const uint32_t code = vxo_argmax(masked, sv);
+    if (sem_out) sem_out[f] = code;
+    if (ac_out) memcpy(ac_out + (size_t)f * na, e->acoustic_codes, (size_t)na * 4);
+    if (x_out) memcpy(x_out + (size_t)f * na, e->x_t, (size_t)na * 4);
+    if (normed_out) memcpy(normed_out + (size_t)f * d, e->normed, (size_t)d * 4);
+    if (logits_out) memcpy(logits_out + (size_t)f * sv, e->semantic_logits, (size_t)sv * 4);
+    const int forced = forced_sem && forced_ac && f < n_forced;
+    if (code <= 1 && !ignore_eos && !forced) break;
+    frames++;
+    /* the state the next frame embeds (:2573-2575; acoustic codes stay in
+     * W.acoustic_codes from fmForward) */
+    if (forced) {
+      e->semantic_argmax = forced_sem[f];
+      memcpy(e->acoustic_codes, forced_ac + (size_t)f * na, (size_t)na * 4);
+    } else {
+      e->semantic_argmax = code;
+    }
+  }
+  free(noise);
+  free(masked);
+  return frames;
+}

@@ -135,6 +135,14 @@ void vxo_fm_forward(vxo_engine *e, const float *noise);
  * read, time projection hoisted out of the frame.  Same arithmetic per
  * output element as vxo_fm_forward. */
 void vxo_fm_forward_batched(vxo_engine *e, const float *noise);
+/* generate() up to the codec decode (src/engine.ts:2416-2585) with the greedy
+ * masked semantic code, device-stream noise and optional teacher forcing;
+ * returns framesGenerated (see vx_oracle.c for the outputs). */
+int vxo_generate(vxo_engine *e, const int32_t *tokens, int n_tokens, int audio_start,
+                 int audio_count, const float *voice, int max_frames, uint64_t noise_seed,
+                 int ignore_eos, const uint32_t *forced_sem, const uint32_t *forced_ac,
+                 int n_forced, uint32_t *sem_out, uint32_t *ac_out, float *x_out,
+                 float *normed_out, float *logits_out);
 
 /* ------------------------------------------------------- codec decoder */
 /* vx_oracle_codec.c: codecDecode (src/engine.ts:1402-1713) and its shaders

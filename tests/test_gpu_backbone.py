@@ -91,6 +91,24 @@ def test_code_and_position_argument_errors(pair1):
     with pytest.raises(V.VoxtralError, match="max_seq_len"):
         g.backbone_step(token=1)
     g.position = 0
+    # KV row ranges whose end overflows int32 (checked in 64 bits)
+    big = 2**31 - 8
+    with pytest.raises(V.VoxtralError, match="KV range"):
+        g.read_kv(0, 0, big, 16)
+    with pytest.raises(V.VoxtralError, match="KV range"):
+        g.write_kv(0, 0, big, np.zeros((16, 1024), np.float32))
+    # voice ranges whose end overflows int32
+    with pytest.raises(V.VoxtralError, match="bad prefill arguments"):
+        g.prefill([1, 2, 3], audio_token_start=big, audio_token_count=64,
+                  voice_embeddings=np.zeros((64, 3072), np.float32))
+    with pytest.raises(V.VoxtralError, match="voice range"):
+        g.generate([1, 2, 3], big, 64, np.zeros((64, 3072), np.float32), 1)
+    # sampling options that would make NaN probabilities
+    for bad in (dict(temperature=0.0), dict(temperature=float("nan")), dict(top_p=0.0),
+                dict(top_p=float("nan")), dict(top_p=1.5), dict(temperature=float("inf"))):
+        with pytest.raises(V.VoxtralError, match="top-p sampling needs"):
+            g.generate([1, 2, 3], 0, 0, None, 1, sampling="top_p", **bad)
+    assert g.position == 0
 
 
 def test_single_layer_decode_at_128(pair1):

@@ -150,3 +150,70 @@ const m = require({json.dumps(JS)});
     finally:
         g.destroy()
     assert np.array_equal(np.float32(r["normed"]), normed[:8])
+
+
+def test_numeric_arguments_are_range_checked():
+    """Numbers that cannot be what the C ABI takes (NaN, fractions, values
+    outside int32, negative frame counts or seeds) throw RangeError before
+    any cast; no GPU is needed for these checks, which come first."""
+    out = run_node(f"""
+const m = require({json.dumps(JS)});
+const n = m.native;
+const res = {{}};
+const tryit = (k, f) => {{ try {{ f(); res[k] = 'ok'; }} catch (e) {{ res[k] = e.constructor.name + ': ' + e.message; }} }};
+tryit('create_nan', () => n.create({{nLayers: NaN}}, 64));
+tryit('create_frac', () => n.create({{nLayers: 1.5}}, 64));
+tryit('create_big', () => n.create(null, 2 ** 40));
+console.log(JSON.stringify(res));
+""")
+    r = json.loads(out.strip().splitlines()[-1])
+    assert r["create_nan"] == "RangeError: nLayers out of range"
+    assert r["create_frac"] == "RangeError: nLayers out of range"
+    assert r["create_big"] == "RangeError: maxSeqLen out of range"
+
+
+@pytest.mark.gpu
+def test_calls_during_a_pending_generate():
+    """While generate() runs on the worker thread, a second generate()
+    rejects, other calls throw, and destroy() is deferred until the pending
+    generate() has completed: it still resolves, and the handle is dead
+    afterwards.  Out-of-range options reject before anything runs."""
+    script = f"""
+const m = require({json.dumps(JS)});
+(async () => {{
+  const e = new m.VoxtralEngine({{config: {{backbone: {{n_layers: 2}}}}, maxSeqLen: 64}});
+  await e.init();
+  e.initSynthetic(0, 0.02);
+  const out = {{}};
+  const msg = async (f) => {{ try {{ await f(); return 'ok'; }} catch (x) {{ return x.constructor.name + ': ' + x.message; }} }};
+  out.bad_frames = await msg(() => e.generate([1, 25, 24], 2, 0, null, -1));
+  out.bad_seed = await msg(() => e.generate([1, 25, 24], 2, 0, null, 2, null, null, {{seed: 0.5}}));
+  out.bad_temp = await msg(() => e.generate([1, 25, 24], 2, 0, null, 2, null, null, {{temperature: 0}}));
+  out.bad_topp = await msg(() => e.generate([1, 25, 24], 2, 0, null, 2, null, null, {{topP: NaN}}));
+  const p = e.generate([1, 25, 24, 24, 35, 500, 24], 2, 0, null, 6, null, null,
+                       {{sampling: 'greedy', seed: 1, ignoreEos: true}});
+  out.second = await msg(() => e.generate([1, 25, 24], 2, 0, null, 2));
+  out.reset = await msg(() => e.reset());
+  out.step = await msg(() => e.debugBackboneStepFull(24));
+  out.ready = e.isReady;
+  const h = e._h;
+  e.destroy();
+  out.destroyed_early = await msg(() => m.native.reset(h));
+  const r = await p;
+  out.frames = r.stats.framesGenerated;
+  out.after = await msg(() => m.native.reset(h));
+  console.log(JSON.stringify(out));
+}})().catch((err) => {{ console.error(err); process.exit(3); }});
+"""
+    print("[napi] calls during a pending generate", flush=True)
+    r = json.loads(run_node(script, timeout=300).strip().splitlines()[-1])
+    assert r["bad_frames"] == "RangeError: maxFrames out of range"
+    assert r["bad_seed"] == "RangeError: seed out of range"
+    assert r["bad_temp"].startswith("Error: ") and "temperature" in r["bad_temp"]
+    assert r["bad_topp"].startswith("Error: ") and "top_p" in r["bad_topp"]
+    assert r["second"] == "Error: generate() is still running on this engine"
+    assert r["reset"] == "Error: generate() is still running on this engine"
+    assert r["step"] == "Error: generate() is still running on this engine"
+    assert r["ready"] is True
+    assert r["frames"] == 6
+    assert r["destroyed_early"] == r["after"] == "Error: engine destroyed"

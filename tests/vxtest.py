@@ -57,3 +57,35 @@ def masked_tree_argmax(logits):
     x[0] = -np.inf
     x[8194:] = -np.inf
     return O.argmax(x)
+
+
+VOICE_ROWS = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
+                                        "ar_male_voice_rows64.f32")
+
+
+def voice_rows(n=64):
+    """The reference's real voice embedding rows (ar_male, f32 [n][3072]),
+    from the committed slice (tests/golden/make_voice_rows.py)."""
+    a = np.fromfile(VOICE_ROWS, dtype="<f4").reshape(-1, 3072)
+    assert n <= a.shape[0]
+    return a[:n].copy()
+
+
+def tts_prompt(n_tokens=256, n_voice=64, seed=0):
+    """A prompt laid out as buildTTSPrompt does (src/tokenizer.ts:130-165):
+    BOS [BEGIN_AUDIO] [AUDIO] x n_voice [NEXT_AUDIO_TEXT] text
+    [REPEAT_AUDIO_TEXT] [BEGIN_AUDIO], with the text ids drawn uniformly
+    from the non-special vocabulary.  Returns (tokens, audio_start, count)."""
+    n_text = n_tokens - n_voice - 5
+    assert n_text >= 0
+    rng = np.random.default_rng(seed)
+    text = rng.integers(1000, 131072, n_text).tolist()
+    toks = [1, 25] + [24] * n_voice + [36] + text + [35, 25]
+    return toks, 2, n_voice
+
+
+def fsq_margin(x):
+    """distance of x from the nearest FSQ rounding boundary, in code units
+    (codes are round((clip(x)+1)/2*20)+2, boundaries at half-integers)"""
+    u = (np.clip(np.asarray(x, np.float64), -1, 1) + 1) * 10
+    return np.abs(u - np.floor(u) - 0.5)

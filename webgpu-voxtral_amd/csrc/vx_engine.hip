@@ -1336,7 +1336,7 @@ static int kv_io(vx_engine *e, int32_t layer, int32_t which, int32_t pos0, int32
                  float *host, bool write) {
   if (!e || !host) return VX_E_INVALID;
   if (layer < 0 || layer >= e->cfg.n_layers || which < 0 || which > 1 || pos0 < 0 || npos < 0 ||
-      pos0 + npos > e->max_seq)
+      (int64_t)pos0 + npos > e->max_seq)
     return fail(e, VX_E_INVALID, "KV range out of bounds");
   if (npos == 0) return VX_OK;
   char *base = (char *)(which ? e->vc(layer) : e->kc(layer));
@@ -1477,7 +1477,8 @@ int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t au
   if (!e) return VX_E_INVALID;
   int rc = check_ready(e);
   if (rc) return rc;
-  if (n_tokens < 1 || !tokens || audio_count < 0 || (audio_count > 0 && audio_start < 0))
+  if (n_tokens < 1 || !tokens || audio_count < 0 || (audio_count > 0 && audio_start < 0) ||
+      (int64_t)audio_start + audio_count > INT32_MAX)
     return fail(e, VX_E_INVALID, "bad prefill arguments");
   if ((int64_t)e->host_pos + n_tokens > e->max_seq)
     return fail(e, VX_E_RANGE, "prefill passes max_seq_len %d", e->max_seq);
@@ -1555,8 +1556,10 @@ static uint32_t sample_top_p(const float *logits, int n, double top_p, double te
 int vx_sample_top_p(vx_engine *e, const float *logits, int32_t n, int32_t valid, double top_p,
                     double temperature, uint64_t *state, int32_t on_device, uint32_t *code) {
   if (!e || !logits || !state || !code) return VX_E_INVALID;
-  if (n < 2 || n > TP_MAXN || valid < 2 || temperature <= 0.0)
-    return fail(e, VX_E_INVALID, "top-p: n %d, valid %d out of range", n, valid);
+  if (n < 2 || n > TP_MAXN || valid < 2 || !(temperature > 0.0) || !std::isfinite(temperature) ||
+      !(top_p > 0.0) || !(top_p <= 1.0))
+    return fail(e, VX_E_INVALID, "top-p: n %d, valid %d, temperature %g, top_p %g out of range", n,
+                valid, temperature, top_p);
   if (!on_device) {
     std::vector<float> l(logits, logits + n);
     l[0] = -INFINITY;
@@ -1819,6 +1822,18 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
   vx_generate_options opt;
   vx_generate_options_default(&opt);
   if (opt_in) opt = *opt_in;
+  if (opt.sampling != VX_SAMPLE_GREEDY && opt.sampling != VX_SAMPLE_TOP_P &&
+      opt.sampling != VX_SAMPLE_TOP_P_HOST)
+    return fail(e, VX_E_INVALID, "unknown sampling mode %d", opt.sampling);
+  // NaN fails both comparisons
+  if (opt.sampling != VX_SAMPLE_GREEDY &&
+      (!(opt.temperature > 0.0) || !std::isfinite(opt.temperature) || !(opt.top_p > 0.0) ||
+       !(opt.top_p <= 1.0)))
+    return fail(e, VX_E_INVALID, "top-p sampling needs temperature > 0 and top_p in (0, 1] "
+                "(temperature %g, top_p %g)", opt.temperature, opt.top_p);
+  if (audio_count < 0 || (audio_count > 0 && audio_start < 0) ||
+      (int64_t)audio_start + audio_count > INT32_MAX)
+    return fail(e, VX_E_INVALID, "bad voice range (start %d, count %d)", audio_start, audio_count);
   using clk = std::chrono::steady_clock;
   auto ms = [](clk::time_point a, clk::time_point b) {
     return std::chrono::duration<double, std::milli>(b - a).count();

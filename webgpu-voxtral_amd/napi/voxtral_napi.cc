@@ -7,6 +7,7 @@
 // back to the JS thread through thread-safe functions.
 #include <node_api.h>
 
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -46,13 +47,47 @@ bool is_nullish(napi_env env, napi_value v) {
   return t == napi_null || t == napi_undefined;
 }
 
-vx_engine *handle(napi_env env, napi_value v) {
+// One engine handle: the C-ABI engine and the state of a pending generate().
+// A vx_engine serves one caller at a time and generate() runs on a worker
+// thread, so while a generate() is in flight every other call on the handle
+// throws (a second generate() rejects), and destroy() only marks the handle:
+// the engine is freed when the pending generate() has completed.  A handle
+// that is garbage-collected without destroy() frees its engine then.
+struct EngineHandle {
+  vx_engine *e = nullptr;
+  bool busy = false;       // a generate() is running on the worker thread
+  bool destroyed = false;  // destroy() was called
+};
+
+void handle_finalize(napi_env, void *data, void *) {
+  auto *h = static_cast<EngineHandle *>(data);
+  if (h->e && !h->busy) vx_destroy(h->e);
+  delete h;
+}
+
+EngineHandle *handle_of(napi_env env, napi_value v) {
   void *p = nullptr;
   if (napi_get_value_external(env, v, &p) != napi_ok || !p) {
-    napi_throw_type_error(env, nullptr, "invalid or destroyed engine handle");
+    napi_throw_type_error(env, nullptr, "invalid engine handle");
     return nullptr;
   }
-  return static_cast<vx_engine *>(p);
+  auto *h = static_cast<EngineHandle *>(p);
+  if (h->destroyed) {
+    napi_throw_error(env, nullptr, "engine destroyed");
+    return nullptr;
+  }
+  return h;
+}
+
+// the engine behind a handle, for a call that must not overlap generate()
+vx_engine *handle(napi_env env, napi_value v) {
+  EngineHandle *h = handle_of(env, v);
+  if (!h) return nullptr;
+  if (h->busy) {
+    napi_throw_error(env, nullptr, "generate() is still running on this engine");
+    return nullptr;
+  }
+  return h->e;
 }
 
 double num(napi_env env, napi_value v, double dflt = 0) {
@@ -60,6 +95,27 @@ double num(napi_env env, napi_value v, double dflt = 0) {
   if (!is_nullish(env, v)) napi_get_value_double(env, v, &d);
   return d;
 }
+
+// a JS number that must be an integer in [lo, hi] (NaN, infinities, fractions
+// and out-of-range values throw a RangeError naming `what`); null/undefined
+// give dflt
+bool int_arg(napi_env env, napi_value v, double lo, double hi, const char *what, double dflt,
+             double *out) {
+  double d = dflt;
+  if (!is_nullish(env, v) && napi_get_value_double(env, v, &d) != napi_ok) {
+    napi_throw_type_error(env, nullptr, (std::string(what) + " must be a number").c_str());
+    return false;
+  }
+  if (!std::isfinite(d) || d != std::floor(d) || d < lo || d > hi) {
+    napi_throw_range_error(env, nullptr, (std::string(what) + " out of range").c_str());
+    return false;
+  }
+  *out = d;
+  return true;
+}
+constexpr double kI32Min = -2147483648.0, kI32Max = 2147483647.0, kU32Max = 4294967295.0;
+// seeds: integers in [0, 2^64)
+constexpr double kU64Lim = 18446744073709549568.0;  // largest double below 2^64
 
 std::string str(napi_env env, napi_value v) {
   size_t n = 0;
@@ -141,25 +197,49 @@ napi_value create(napi_env env, napi_callback_info info) {
       if (!has) continue;
       napi_value v;
       napi_get_named_property(env, a.v[0], f.k, &v);
-      double d = num(env, v);
-      if (f.i) *f.i = (int32_t)d;
-      else *f.f = (float)d;
+      if (f.i) {
+        double d = 0;
+        if (!int_arg(env, v, kI32Min, kI32Max, f.k, 0, &d)) return nullptr;
+        *f.i = (int32_t)d;
+      } else {
+        *f.f = (float)num(env, v);
+      }
     }
   }
-  int32_t max_seq = a.n > 1 ? (int32_t)num(env, a.v[1], 4096) : 4096;
+  double ms = 4096;
+  if (a.n > 1 && !int_arg(env, a.v[1], kI32Min, kI32Max, "maxSeqLen", 4096, &ms)) return nullptr;
   vx_engine *e = nullptr;
-  int rc = vx_create(&c, max_seq, &e);
+  int rc = vx_create(&c, (int32_t)ms, &e);
   if (rc) return throw_vx(env, nullptr, rc);
+  auto *eh = new EngineHandle();
+  eh->e = e;
   napi_value h;
-  NAPI_OK(env, napi_create_external(env, e, nullptr, nullptr, &h));
+  if (napi_create_external(env, eh, handle_finalize, nullptr, &h) != napi_ok) {
+    vx_destroy(e);
+    delete eh;
+    napi_throw_error(env, nullptr, "N-API call failed: napi_create_external");
+    return nullptr;
+  }
   return h;
 }
 
+// destroy(h): frees the engine now, or, while a generate() is running, as
+// soon as it completes; the handle is unusable from here on
 napi_value destroy(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a) || a.n < 1) return nullptr;
-  vx_engine *e = handle(env, a.v[0]);
-  if (e) vx_destroy(e);
+  void *p = nullptr;
+  if (napi_get_value_external(env, a.v[0], &p) != napi_ok || !p) {
+    napi_throw_type_error(env, nullptr, "invalid engine handle");
+    return nullptr;
+  }
+  auto *h = static_cast<EngineHandle *>(p);
+  if (h->destroyed) return nullptr;
+  h->destroyed = true;
+  if (!h->busy && h->e) {
+    vx_destroy(h->e);
+    h->e = nullptr;
+  }
   return nullptr;
 }
 
@@ -179,7 +259,9 @@ napi_value load_tensor(napi_env env, napi_callback_info info) {
   for (uint32_t i = 0; i < nd; i++) {
     napi_value x;
     napi_get_element(env, a.v[3], i, &x);
-    shape[i] = (int64_t)num(env, x);
+    double d = 0;
+    if (!int_arg(env, x, 0, 9007199254740991.0, "shape", 0, &d)) return nullptr;
+    shape[i] = (int64_t)d;
   }
   int rc = vx_load_tensor(e, name.c_str(), data, n, shape.data(), (int32_t)nd);
   if (rc) return throw_vx(env, e, rc);
@@ -221,8 +303,10 @@ napi_value codec_decode(napi_env env, napi_callback_info info) {
     napi_throw_range_error(env, nullptr, "acousticCodes must hold 36 codes per frame");
     return nullptr;
   }
-  const int32_t stop = a.n > 3 && !is_nullish(env, a.v[3]) ? (int32_t)num(env, a.v[3])
-                                                           : VX_CODEC_STOP_AUDIO;
+  double sd = VX_CODEC_STOP_AUDIO;
+  if (a.n > 3 && !int_arg(env, a.v[3], kI32Min, kI32Max, "stop", VX_CODEC_STOP_AUDIO, &sd))
+    return nullptr;
+  const int32_t stop = (int32_t)sd;
   std::vector<float> out(std::max<size_t>(vx_codec_stop_count((int32_t)ns, stop), 1));
   int rc = vx_codec_decode_debug(e, sem, ac, (int32_t)ns, stop, out.data(), out.size());
   if (rc) return throw_vx(env, e, rc);
@@ -250,7 +334,9 @@ napi_value tokenizer_create(napi_env env, napi_callback_info info) {
   }
   std::vector<int64_t> off64(off, off + no);
   vx_tokenizer *t = nullptr;
-  int rc = vx_tokenizer_create(blob, off64.data(), ranks, (int32_t)nr, (int32_t)num(env, a.v[3]), &t);
+  double ns = 0;
+  if (!int_arg(env, a.v[3], 0, kI32Max, "numSpecial", 0, &ns)) return nullptr;
+  int rc = vx_tokenizer_create(blob, off64.data(), ranks, (int32_t)nr, (int32_t)ns, &t);
   if (rc) return throw_vx(env, nullptr, rc);
   napi_value h;
   NAPI_OK(env, napi_create_external(env, t, tokenizer_finalize, nullptr, &h));
@@ -294,7 +380,9 @@ napi_value init_synthetic(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, a) || a.n < 3) return nullptr;
   vx_engine *e = handle(env, a.v[0]);
   if (!e) return nullptr;
-  int rc = vx_init_synthetic(e, (uint64_t)num(env, a.v[1]), (float)num(env, a.v[2], 0.02));
+  double seed = 0;
+  if (!int_arg(env, a.v[1], 0, kU64Lim, "seed", 0, &seed)) return nullptr;
+  int rc = vx_init_synthetic(e, (uint64_t)seed, (float)num(env, a.v[2], 0.02));
   if (rc) return throw_vx(env, e, rc);
   return nullptr;
 }
@@ -302,8 +390,9 @@ napi_value init_synthetic(napi_env env, napi_callback_info info) {
 napi_value is_ready(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a) || a.n < 1) return nullptr;
-  vx_engine *e = handle(env, a.v[0]);
-  if (!e) return nullptr;
+  EngineHandle *h = handle_of(env, a.v[0]);  // weight flags only: fine during generate()
+  if (!h) return nullptr;
+  vx_engine *e = h->e;
   napi_value b;
   napi_get_boolean(env, vx_is_ready(e) != 0, &b);
   return b;
@@ -325,7 +414,9 @@ napi_value position(napi_env env, napi_callback_info info) {
   vx_engine *e = handle(env, a.v[0]);
   if (!e) return nullptr;
   if (a.n > 1 && !is_nullish(env, a.v[1])) {
-    int rc = vx_set_position(e, (int32_t)num(env, a.v[1]));
+    double p = 0;
+    if (!int_arg(env, a.v[1], kI32Min, kI32Max, "position", 0, &p)) return nullptr;
+    int rc = vx_set_position(e, (int32_t)p);
     if (rc) return throw_vx(env, e, rc);
   }
   napi_value v;
@@ -355,7 +446,11 @@ napi_value backbone_step(napi_env env, napi_callback_info info) {
   napi_get_value_bool(env, a.v[4], &lm);
   uint32_t am = 0;
   std::vector<float> normed(3072);
-  int rc = vx_backbone_step(e, (int32_t)num(env, a.v[1]), (int32_t)num(env, a.v[2]), pre, lm ? 1 : 0,
+  double tok = 0, mode = 0;
+  if (!int_arg(env, a.v[1], kI32Min, kI32Max, "tokenId", 0, &tok) ||
+      !int_arg(env, a.v[2], kI32Min, kI32Max, "embedMode", 0, &mode))
+    return nullptr;
+  int rc = vx_backbone_step(e, (int32_t)tok, (int32_t)mode, pre, lm ? 1 : 0,
                             &am, normed.data());
   if (rc) return throw_vx(env, e, rc);
   napi_value out;
@@ -399,7 +494,9 @@ napi_value set_semantic_code(napi_env env, napi_callback_info info) {
   if (!get_args(env, info, a) || a.n < 2) return nullptr;
   vx_engine *e = handle(env, a.v[0]);
   if (!e) return nullptr;
-  int rc = vx_set_semantic_code(e, (uint32_t)num(env, a.v[1]));
+  double code = 0;
+  if (!int_arg(env, a.v[1], 0, kU32Max, "semanticCode", 0, &code)) return nullptr;
+  int rc = vx_set_semantic_code(e, (uint32_t)code);
   if (rc) return throw_vx(env, e, rc);
   return nullptr;
 }
@@ -411,7 +508,9 @@ napi_value read(napi_env env, napi_callback_info info) {
   vx_engine *e = handle(env, a.v[0]);
   if (!e) return nullptr;
   std::string name = str(env, a.v[1]);
-  std::vector<float> buf((size_t)num(env, a.v[2], 16));
+  double cnt = 16;
+  if (!int_arg(env, a.v[2], 0, 1 << 28, "count", 16, &cnt)) return nullptr;
+  std::vector<float> buf((size_t)cnt);
   int rc = vx_read(e, name.c_str(), buf.data(), buf.size());
   if (rc) return throw_vx(env, e, rc);
   return new_f32(env, buf.data(), buf.size());
@@ -434,6 +533,8 @@ struct Msg {
 
 struct GenJob {
   vx_engine *e;
+  EngineHandle *h;              // busy while the job runs
+  napi_ref handle_ref = nullptr;  // keeps the handle alive until the job is done
   std::vector<int32_t> tokens;
   int32_t audio_start, audio_count, max_frames;
   std::vector<float> voice;
@@ -514,9 +615,17 @@ void dispatch(napi_env env, napi_value, void *context, void *data) {
       else napi_create_double(env, m->done_ms, &argv[1]);
       napi_call_function(env, undef, cb, 2, argv, nullptr);
     } else if (m->kind == MSG_DONE) {
+      // the engine is free again before the promise's continuations run; a
+      // destroy() that arrived meanwhile frees it now
+      j->h->busy = false;
+      if (j->h->destroyed && j->h->e) {
+        vx_destroy(j->h->e);
+        j->h->e = nullptr;
+      }
       settle(env, j);
       if (j->on_frame) napi_delete_reference(env, j->on_frame);
       if (j->on_stage) napi_delete_reference(env, j->on_stage);
+      if (j->handle_ref) napi_delete_reference(env, j->handle_ref);
       napi_release_threadsafe_function(j->events, napi_tsfn_release);
       delete m;
       delete j;
@@ -573,10 +682,11 @@ napi_value generate(napi_env env, napi_callback_info info) {
     napi_throw_type_error(env, nullptr, "generate needs at least 6 arguments");
     return nullptr;
   }
-  vx_engine *e = handle(env, a.v[0]);
+  vx_engine *e = handle(env, a.v[0]);  // throws while another generate() runs
   if (!e) return nullptr;
   auto *j = new GenJob();
   j->e = e;
+  j->h = handle_of(env, a.v[0]);
   bool is_ta = false;
   napi_is_typedarray(env, a.v[1], &is_ta);
   if (is_ta) {
@@ -594,11 +704,22 @@ napi_value generate(napi_env env, napi_callback_info info) {
     for (uint32_t i = 0; i < nt; i++) {
       napi_value x;
       napi_get_element(env, a.v[1], i, &x);
-      j->tokens[i] = (int32_t)num(env, x);
+      double t = 0;
+      if (!int_arg(env, x, kI32Min, kI32Max, "token", 0, &t)) {
+        delete j;
+        return nullptr;
+      }
+      j->tokens[i] = (int32_t)t;
     }
   }
-  j->audio_start = (int32_t)num(env, a.v[2]);
-  j->audio_count = (int32_t)num(env, a.v[3]);
+  double as = 0, ac = 0;
+  if (!int_arg(env, a.v[2], kI32Min, kI32Max, "audioTokenStart", 0, &as) ||
+      !int_arg(env, a.v[3], 0, kI32Max, "audioTokenCount", 0, &ac)) {
+    delete j;
+    return nullptr;
+  }
+  j->audio_start = (int32_t)as;
+  j->audio_count = (int32_t)ac;
   j->has_voice = !is_nullish(env, a.v[4]);
   if (j->has_voice) {
     size_t n = 0;
@@ -614,7 +735,12 @@ napi_value generate(napi_env env, napi_callback_info info) {
       return nullptr;
     }
   }
-  j->max_frames = (int32_t)num(env, a.v[5], 500);
+  double mf = 500;
+  if (!int_arg(env, a.v[5], 0, kI32Max, "maxFrames", 500, &mf)) {
+    delete j;
+    return nullptr;
+  }
+  j->max_frames = (int32_t)mf;
   vx_generate_options_default(&j->opt);
   if (a.n > 6 && !is_nullish(env, a.v[6])) {
     napi_value v;
@@ -623,6 +749,11 @@ napi_value generate(napi_env env, napi_callback_info info) {
     if (has) {
       napi_get_named_property(env, a.v[6], "sampling", &v);
       const std::string m = str(env, v);
+      if (m != "greedy" && m != "top_p" && m != "top_p_host") {
+        delete j;
+        napi_throw_range_error(env, nullptr, "sampling must be 'top_p', 'top_p_host' or 'greedy'");
+        return nullptr;
+      }
       j->opt.sampling = m == "greedy" ? VX_SAMPLE_GREEDY
                         : m == "top_p_host" ? VX_SAMPLE_TOP_P_HOST : VX_SAMPLE_TOP_P;
     }
@@ -638,8 +769,13 @@ napi_value generate(napi_env env, napi_callback_info info) {
         bool b = false;
         napi_get_value_bool(env, v, &b);
         d = b;
+      } else if (k == 2) {
+        if (!int_arg(env, v, 0, kU64Lim, "seed", 0, &d)) {
+          delete j;
+          return nullptr;
+        }
       } else {
-        d = num(env, v);
+        d = num(env, v);  // topP / temperature: the library rejects bad values
       }
       if (k == 0) j->opt.top_p = d;
       if (k == 1) j->opt.temperature = d;
@@ -658,6 +794,8 @@ napi_value generate(napi_env env, napi_callback_info info) {
     napi_throw_error(env, nullptr, "could not create the generate event queue");
     return nullptr;
   }
+  napi_create_reference(env, a.v[0], 1, &j->handle_ref);
+  j->h->busy = true;
   napi_create_promise(env, &j->deferred, &promise);
   napi_create_async_work(env, nullptr, name, gen_execute, gen_complete, j, &j->work);
   napi_queue_async_work(env, j->work);
