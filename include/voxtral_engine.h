@@ -291,6 +291,18 @@ int vx_sample_top_p(vx_engine *e, const float *logits, int32_t n, int32_t valid,
                     double top_p, double temperature, uint64_t *state,
                     int32_t on_device, uint32_t *code);
 
+/* No counterpart in the reference.  For callers that cannot allocate
+ * device memory (tight serving loops, harnesses that forbid hipMalloc): the
+ * device path of vx_sample_top_p, with no engine and no allocation.  Its
+ * staging (logits, parameters, state, code: 37 KB) is a file-scope device
+ * array of the library, one per GPU, so n is at most 9216 (larger n returns
+ * VX_E_RANGE).  Runs on the null stream of the current device and waits for
+ * it.  Calls that overlap on one GPU share the array and race.  Errors are
+ * read with vx_last_error(NULL). */
+int vx_sample_top_p_noalloc(const float *logits, int32_t n, int32_t valid,
+                            double top_p, double temperature, uint64_t *state,
+                            uint32_t *code);
+
 /* ------------------------------------------------------ measurement */
 /* No reference counterparts (the reference times on the CPU,
  * src/benchmark.ts:277-320).  Each runs on the handle's stream, bracketed

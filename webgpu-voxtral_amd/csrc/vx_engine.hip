@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -583,6 +584,49 @@ static int prepare_input(vx_engine *e, int32_t token, int32_t mode, const float 
   }
   LAUNCHCHK(e);
   return VX_OK;
+}
+
+// ------------------------------------------ allocation-free top-p staging
+// vx_sample_top_p_noalloc stages its operands in this file-scope device
+// array instead of an engine's allocation: the caller's logits (at most
+// TP_MAXN), the (top_p, temperature) pair, the splitmix64 state and the
+// picked code.  Every GPU holds its own copy until the process ends.  Host
+// code never passes `scratch` itself to a kernel or a copy (in host code the
+// name is only a stand-in): the device address comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+namespace {
+constexpr size_t NA_LOGITS = 0;
+constexpr size_t NA_PARAMS = NA_LOGITS + (size_t)TP_MAXN * 4;  // 2 doubles
+constexpr size_t NA_STATE = NA_PARAMS + 16;                    // u64
+constexpr size_t NA_CODE = NA_STATE + 8;                       // u32
+constexpr size_t NA_BYTES = (NA_CODE + 4 + 255) & ~size_t(255);
+static_assert(NA_PARAMS % 8 == 0 && NA_STATE % 8 == 0, "staging alignment");
+constexpr int NA_MAX_DEVICES = 64;
+std::mutex g_na_mu;
+char *g_na_ptr[NA_MAX_DEVICES] = {};
+}  // namespace
+static __device__ __align__(256) unsigned char scratch[NA_BYTES];
+
+// the array's address on the current device (looked up on the first call
+// there); nullptr and g_create_error set on failure
+static char *noalloc_scratch() {
+  int dev = -1;
+  hipError_t s = hipGetDevice(&dev);
+  if (s != hipSuccess || dev < 0 || dev >= NA_MAX_DEVICES) {
+    fail(nullptr, VX_E_DEVICE, "no current HIP device (%s)", hipGetErrorString(s));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_na_mu);
+  if (!g_na_ptr[dev]) {
+    void *p = nullptr;
+    s = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (s != hipSuccess || !p) {
+      fail(nullptr, VX_E_DEVICE, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(s));
+      return nullptr;
+    }
+    g_na_ptr[dev] = (char *)p;
+  }
+  return g_na_ptr[dev];
 }
 
 // ================================================================ C ABI
@@ -1577,6 +1621,43 @@ int vx_sample_top_p(vx_engine *e, const float *logits, int32_t n, int32_t valid,
   HIPCHK(e, hipMemcpyAsync(code, e->argmax_res, 4, hipMemcpyDeviceToHost, e->st));
   HIPCHK(e, hipMemcpyAsync(state, e->rng_state, 8, hipMemcpyDeviceToHost, e->st));
   HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+// vx_sample_top_p's device path with its staging in the file-scope array
+// above: no engine, no allocation.  Runs on the null stream of the current
+// device and waits for it.  Calls that overlap on one GPU share the array
+// and race.
+int vx_sample_top_p_noalloc(const float *logits, int32_t n, int32_t valid, double top_p,
+                            double temperature, uint64_t *state, uint32_t *code) {
+  if (!logits || !state || !code) return fail(nullptr, VX_E_INVALID, "NULL argument");
+  if (n > TP_MAXN)
+    return fail(nullptr, VX_E_RANGE,
+                "top-p: %d logits exceed the %d of the allocation-free sampler's device buffer", n,
+                TP_MAXN);
+  if (n < 2 || valid < 2 || !(temperature > 0.0) || !std::isfinite(temperature) ||
+      !(top_p > 0.0) || !(top_p <= 1.0))
+    return fail(nullptr, VX_E_INVALID, "top-p: n %d, valid %d, temperature %g, top_p %g out of range",
+                n, valid, temperature, top_p);
+  char *base = noalloc_scratch();
+  if (!base) return VX_E_DEVICE;
+  float *d_logits = (float *)(base + NA_LOGITS);
+  double *d_params = (double *)(base + NA_PARAMS);
+  uint64_t *d_state = (uint64_t *)(base + NA_STATE);
+  uint32_t *d_code = (uint32_t *)(base + NA_CODE);
+  const double params[2] = {top_p, temperature};
+  hipStream_t st = nullptr;
+  // every operand the kernel reads is written first: nothing stale from an
+  // earlier call is used
+  HIPCHK(nullptr, hipMemcpyAsync(d_logits, logits, (size_t)n * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(nullptr, hipMemcpyAsync(d_params, params, sizeof params, hipMemcpyHostToDevice, st));
+  HIPCHK(nullptr, hipMemcpyAsync(d_state, state, 8, hipMemcpyHostToDevice, st));
+  hipLaunchKernelGGL(topp_sample_kernel, dim3(1), dim3(TP_NT), 0, st, d_logits, n, valid, d_params,
+                     d_state, d_code);
+  LAUNCHCHK(nullptr);
+  HIPCHK(nullptr, hipMemcpyAsync(code, d_code, 4, hipMemcpyDeviceToHost, st));
+  HIPCHK(nullptr, hipMemcpyAsync(state, d_state, 8, hipMemcpyDeviceToHost, st));
+  HIPCHK(nullptr, hipStreamSynchronize(st));
   return VX_OK;
 }
 

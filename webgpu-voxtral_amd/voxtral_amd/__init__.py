@@ -88,6 +88,7 @@ _SIGS = {
     "vx_f32_to_f16_trunc": (None, [_VP, _VP, ctypes.c_size_t]),
     "vx_sample_top_p": (_I32, [_VP, _VP, _I32, _I32, ctypes.c_double, ctypes.c_double, _VP, _I32,
                                _VP]),
+    "vx_sample_top_p_noalloc": (_I32, [_VP, _I32, _I32, ctypes.c_double, ctypes.c_double, _VP, _VP]),
     "vx_reset": (_I32, [_VP]),
     "vx_position": (_I32, [_VP]),
     "vx_set_position": (_I32, [_VP, _I32]),
@@ -157,6 +158,21 @@ def f32_to_f16_trunc(values):
     out = np.empty(a.shape, np.uint16)
     load_library().vx_f32_to_f16_trunc(a.ctypes.data, out.ctypes.data, a.size)
     return out
+
+
+def sample_top_p_noalloc(logits, valid, top_p, temperature, state):
+    """The device top-p of VoxtralEngine.sample_top_p without an engine or
+    any allocation (vx_sample_top_p_noalloc: the library's own staging array,
+    at most 9216 logits); returns (code, next splitmix64 state)."""
+    L = load_library()
+    lg = np.ascontiguousarray(logits, np.float32)
+    st = ctypes.c_uint64(state)
+    code = ctypes.c_uint32()
+    rc = L.vx_sample_top_p_noalloc(lg.ctypes.data, lg.size, int(valid), float(top_p),
+                                   float(temperature), ctypes.byref(st), ctypes.byref(code))
+    if rc != VX_OK:
+        raise VoxtralError(rc, L.vx_last_error(None).decode())
+    return code.value, st.value
 
 
 def default_config(**over):
