@@ -113,7 +113,9 @@ def measure_prompt(eng, reps=5):
     pf = float(np.median(times[1:]))
     useful = TOKEN_FLOP * 256
     issued = useful * 2  # hi and lo halves of the activations
-    ms = eng.time_backbone_steps(500, hold_position=False)
+    # each step's input is the previous step's W.normed (the precomputed-
+    # embedding path), the prompt configuration's decode tail
+    ms = eng.time_backbone_steps(500, feedback=True)
     fps = 500 * 1000.0 / ms
     return {"prefill_ms": round(pf * 1e3, 3), "prefill_tokens_per_s": round(256 / pf, 1),
             "useful_TFLOPs": round(useful / pf / 1e12, 2),
@@ -122,7 +124,8 @@ def measure_prompt(eng, reps=5):
             "decode_steps": 500, "decode_ms_per_step": round(ms / 500, 5),
             "decode_frames_per_s": round(fps, 2),
             "note": "prefill timed on the host clock around vx_prefill (host copies of 256 ids and "
-                    "64 voice rows included), median of 4 after 1 warm-up"}
+                    "64 voice rows included), median of 4 after 1 warm-up; decode steps fed "
+                    "back through W.normed as the precomputed embedding, HIP events"}
 
 
 def measure_codec(eng, T=250, reps=3):

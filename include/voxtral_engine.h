@@ -308,13 +308,21 @@ int vx_sample_top_p_noalloc(const float *logits, int32_t n, int32_t valid,
  * src/benchmark.ts:277-320).  Each runs on the handle's stream, bracketed
  * by HIP events, inputs resident in HBM. */
 
-/* n backbone decode steps (graph replays), each starting from the hidden
- * state the previous step left; LM head off.  *ms = total event time.
- * hold_position = 0: positions advance by n (the context grows);
- * hold_position != 0: every step decodes at the current position (reads
- * the same number of keys, rewrites that KV row) and position stays. */
-int vx_time_backbone_steps(vx_engine *e, int32_t n, int32_t hold_position,
-                           float *ms);
+/* n backbone decode steps (graph replays); LM head off.  *ms = total event
+ * time.  mode:
+ *   VX_TIME_ADVANCE   each step starts from the residual stream the previous
+ *                     step left; positions advance by n (the context grows);
+ *   VX_TIME_HOLD      the same, but every step decodes at the current
+ *                     position (reads the same number of keys, rewrites that
+ *                     KV row) and the position stays;
+ *   VX_TIME_FEEDBACK  positions advance, and each step's input embedding is
+ *                     the previous step's W.normed, taken through the
+ *                     precomputed-embedding path (src/engine.ts:847-854): a
+ *                     prompt's decode tail fed with each frame's output. */
+#define VX_TIME_ADVANCE 0
+#define VX_TIME_HOLD 1
+#define VX_TIME_FEEDBACK 2
+int vx_time_backbone_steps(vx_engine *e, int32_t n, int32_t mode, float *ms);
 /* n frames of the full loop (multi-codebook embed + backbone + FM, greedy
  * codes on the device, no EOS), as one graph replay each. */
 int vx_time_frames(vx_engine *e, int32_t n, float *ms);

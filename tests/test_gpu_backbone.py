@@ -361,3 +361,33 @@ def test_long_context_decode(kv_f16):
     finally:
         g.destroy()
         o.close()
+
+
+def test_long_context_decode_26_layers_f16_kv():
+    """The long-context stress as specified: the full 26-layer backbone with
+    the f16 KV cache, decoding consecutive positions 3896..3899 over a
+    synthetic N(0,1) cache.  The cache is filled with the same f16 values on
+    both sides (the oracle holds them exactly as f32), so only the rounding
+    of each step's new K/V row to f16 can differ (one f16 ulp where the f32
+    values of the two summation orders straddle a rounding boundary).
+    Hidden states to the 1e-2 bar at every step."""
+    print("[long] 26-layer engines, f16 KV, positions 3896..3899", flush=True)
+    g = gpu_engine(n_layers=26, max_seq=4096, kv_f16=True)
+    o = oracle_engine(n_layers=26, max_seq=4096)
+    try:
+        o.set_kv_f16(True)
+        g.fill_kv_synthetic(SEED, 3896)
+        fill_oracle_kv(o, SEED, 3896)
+        g.position = 3896
+        o.position = 3896
+        for i in range(4):
+            x = O.gen_f32(SEED + 60 + i, "input.hidden", 3072)
+            _, gn = g.backbone_step(precomputed=x)
+            o.backbone_step(precomputed=x)
+            err = max_rel_err(gn, o.buffer("normed"))
+            print(f"[long] position {3896 + i}: normed max rel err {err:.2e}", flush=True)
+            assert err < 1e-2 and ref_allclose(gn, o.buffer("normed")), (i, err)
+        assert g.position == o.position == 3900
+    finally:
+        g.destroy()
+        o.close()

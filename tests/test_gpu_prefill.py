@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from vxtest import gpu_engine, max_rel_err, oracle_engine
+from vxtest import gpu_engine, max_rel_err, oracle_engine, tts_prompt, voice_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -139,3 +139,38 @@ def test_prefill_argument_errors():
         assert g.position == 0
     finally:
         g.destroy()
+
+
+@pytest.mark.parametrize("layers,n_tok,n_voice", [(2, 256, 64), (26, 32, 8)])
+def test_prompt_then_feedback_decode(layers, n_tok, n_voice):
+    """The prompt configuration: a prompt laid out as buildTTSPrompt makes it
+    with the reference's real voice rows (ar_male) spliced at offset 2,
+    prefilled, then decode steps whose input is the previous step's W.normed
+    through the precomputed-embedding path (the device loop the benchmark
+    times, VX_TIME_FEEDBACK), against the oracle doing the same per step."""
+    print(f"[prompt] {layers} layers, {n_tok}-token prompt, {n_voice} voice rows, 4 feedback steps",
+          flush=True)
+    toks, a0, na = tts_prompt(n_tok, n_voice, seed=7)
+    voice = voice_rows(n_voice)
+    g = gpu_engine(n_layers=layers, max_seq=512)
+    o = oracle_engine(n_layers=layers, max_seq=512)
+    try:
+        g.prefill(toks, a0, na, voice)
+        oracle_prefill(o, toks, a0, na, voice)
+        bar = 1e-3 if layers <= 2 else 1e-2
+        assert max_rel_err(g.debug_read("normed", 3072), o.buffer("normed")) < bar
+        g.time_backbone_steps(4, feedback=True)
+        for _ in range(4):
+            o.backbone_step(precomputed=o.buffer("normed").copy())
+        assert g.position == o.position == n_tok + 4
+        err = max_rel_err(g.debug_read("normed", 3072), o.buffer("normed"))
+        print(f"[prompt] normed after the feedback steps: max rel err {err:.2e}", flush=True)
+        assert err < bar
+        for l in (0, layers - 1):
+            for w in (0, 1):
+                got = g.read_kv(l, w, n_tok, 4)
+                ref = o.kv(l, w)[n_tok:n_tok + 4]
+                assert max_rel_err(got, ref) < bar, (l, w)
+    finally:
+        g.destroy()
+        o.close()

@@ -84,7 +84,10 @@ def test_device_host_and_reference_agree(eng):
         state = st_ref
     print(f"device {same_dev}/{trials}, host {same_host}/{trials} equal to the reference")
     assert same_host == trials
-    assert same_dev >= trials - 1  # f64 sums in another order may move one boundary
+    # the device sums the masses exactly (integers), the reference in f64:
+    # a pick can only differ where a running sum lies within f64 rounding of
+    # the drawn threshold, which none of these draws does
+    assert same_dev == trials
 
 
 def test_ties_and_edge_cases(eng):

@@ -120,7 +120,8 @@ struct vx_engine {
   int pf_chunk = PF_MAXT;  // tokens per prefill chunk (multiple of 128)
 
   int host_pos = 0;
-  hipGraphExec_t step_exec = nullptr, hold_exec = nullptr, frame_exec = nullptr,
+  hipGraphExec_t step_exec = nullptr, hold_exec = nullptr, feedback_exec = nullptr,
+                 frame_exec = nullptr,
                  fm_greedy_exec = nullptr, fm_plain_exec = nullptr;
   bool use_graphs = true;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -350,6 +351,18 @@ static void enqueue_backbone_at(vx_engine *e, bool advance) {
 }
 static void enqueue_backbone(vx_engine *e) { enqueue_backbone_at(e, true); }
 static void enqueue_backbone_hold(vx_engine *e) { enqueue_backbone_at(e, false); }
+
+__global__ void copy_dim_kernel(const float *src, float *dst) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < DIM) dst[i] = src[i];
+}
+// A step whose input embedding is the previous step's W.normed, through the
+// precomputed-embedding path (src/engine.ts:847-854): a prompt's decode tail
+// fed with each frame's output hidden state.
+static void enqueue_backbone_feedback(vx_engine *e) {
+  hipLaunchKernelGGL(copy_dim_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->normed, e->x);
+  enqueue_backbone_at(e, true);
+}
 
 static void enqueue_lm_head(vx_engine *e) {
   GemvArgs a = gargs(e->tok_emb, e->normed, DIM, e->logits, 0, e->cfg.vocab_size);
@@ -1009,6 +1022,7 @@ void vx_destroy(vx_engine *e) {
   if (e->st) (void)hipStreamSynchronize(e->st);
   if (e->step_exec) (void)hipGraphExecDestroy(e->step_exec);
   if (e->hold_exec) (void)hipGraphExecDestroy(e->hold_exec);
+  if (e->feedback_exec) (void)hipGraphExecDestroy(e->feedback_exec);
   if (e->fm_greedy_exec) (void)hipGraphExecDestroy(e->fm_greedy_exec);
   if (e->fm_topp_exec) (void)hipGraphExecDestroy(e->fm_topp_exec);
   if (e->frame_topp_exec) (void)hipGraphExecDestroy(e->frame_topp_exec);
@@ -2095,15 +2109,19 @@ int vx_tokenizer_encode_pieces(const vx_tokenizer *t, const uint8_t *bytes,
 }
 
 // ---------------------------------------------------------- measurement
-int vx_time_backbone_steps(vx_engine *e, int32_t n, int32_t hold, float *out_ms) {
-  if (!e || n < 1 || !out_ms) return VX_E_INVALID;
+int vx_time_backbone_steps(vx_engine *e, int32_t n, int32_t mode, float *out_ms) {
+  if (!e || n < 1 || !out_ms || mode < VX_TIME_ADVANCE || mode > VX_TIME_FEEDBACK)
+    return e ? fail(e, VX_E_INVALID, "bad timing arguments") : VX_E_INVALID;
   int rc = check_ready(e);
   if (rc) return rc;
+  const bool hold = mode == VX_TIME_HOLD;
   if ((int64_t)e->host_pos + (hold ? 1 : n) > e->max_seq)
     return fail(e, VX_E_RANGE, "steps pass max_seq_len");
   HIPCHK(e, hipEventRecord(e->ev0, e->st));
   for (int i = 0; i < n; i++) {
-    rc = hold ? run_step_hold(e) : run_step(e);
+    rc = hold ? run_step_hold(e)
+              : mode == VX_TIME_FEEDBACK ? run_seq(e, &e->feedback_exec, enqueue_backbone_feedback)
+                                         : run_step(e);
     if (rc) return rc;
   }
   HIPCHK(e, hipEventRecord(e->ev1, e->st));

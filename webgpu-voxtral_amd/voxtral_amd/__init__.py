@@ -477,10 +477,16 @@ class VoxtralEngine:
         return code.value, st.value
 
     # -- measurement (no reference counterpart) --
-    def time_backbone_steps(self, n, hold_position=False):
+    def time_backbone_steps(self, n, hold_position=False, feedback=False):
+        """n decode steps on the device; returns the event time in ms.
+        hold_position: every step at the current position; feedback: each
+        step's input is the previous step's W.normed (precomputed-embedding
+        path), positions advancing."""
+        if hold_position and feedback:
+            raise ValueError("hold_position and feedback exclude each other")
+        mode = 1 if hold_position else 2 if feedback else 0
         ms = ctypes.c_float()
-        self._check(self._lib.vx_time_backbone_steps(self._h, int(n), int(bool(hold_position)),
-                                                     ctypes.byref(ms)))
+        self._check(self._lib.vx_time_backbone_steps(self._h, int(n), mode, ctypes.byref(ms)))
         return ms.value
 
     def time_frames(self, n):
