@@ -98,10 +98,10 @@ TOKEN_FLOP = 2 * LAYERS * (6144 * 3072 + 3072 * 4096 + 2 * 9216 * 3072 + 3072 * 
 MFMA_PEAK_F16 = 2.5e15  # dense f16 MFMA, MI355X
 
 
-def measure_prompt(eng, reps=5):
+def measure_prompt(eng, reps=5, decode=True):
     """The 256-token prompt with 64 voice rows N(0,1) spliced at offset 2,
-    prefilled as batched GEMMs, then 500 decode steps over the growing
-    context (257..756 keys)."""
+    prefilled as batched GEMMs, then (decode) 500 decode steps over the
+    growing context (257..756 keys)."""
     toks = np.random.default_rng(1).integers(0, 131072, 256)
     voice = np.random.default_rng(2).standard_normal((64, 3072)).astype(np.float32)
     times = []
@@ -113,14 +113,17 @@ def measure_prompt(eng, reps=5):
     pf = float(np.median(times[1:]))
     useful = TOKEN_FLOP * 256
     issued = useful * 2  # hi and lo halves of the activations
+    out = {"prefill_ms": round(pf * 1e3, 3), "prefill_tokens_per_s": round(256 / pf, 1),
+           "useful_TFLOPs": round(useful / pf / 1e12, 2),
+           "mfma_issued_TFLOPs": round(issued / pf / 1e12, 2),
+           "mfma_frac_of_peak": round(issued / pf / MFMA_PEAK_F16, 4)}
+    if not decode:
+        return out
     # each step's input is the previous step's W.normed (the precomputed-
     # embedding path), the prompt configuration's decode tail
     ms = eng.time_backbone_steps(500, feedback=True)
     fps = 500 * 1000.0 / ms
-    return {"prefill_ms": round(pf * 1e3, 3), "prefill_tokens_per_s": round(256 / pf, 1),
-            "useful_TFLOPs": round(useful / pf / 1e12, 2),
-            "mfma_issued_TFLOPs": round(issued / pf / 1e12, 2),
-            "mfma_frac_of_peak": round(issued / pf / MFMA_PEAK_F16, 4),
+    return {**out,
             "decode_steps": 500, "decode_ms_per_step": round(ms / 500, 5),
             "decode_frames_per_s": round(fps, 2),
             "note": "prefill timed on the host clock around vx_prefill (host copies of 256 ids and "
@@ -195,9 +198,11 @@ def main():
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="also run a plain device copy of this many MB (a known-traffic "
                          "kernel for scaling hardware byte counters)")
-    ap.add_argument("--section", choices=["all", "codec"], default="all",
+    ap.add_argument("--section", choices=["all", "codec", "prompt", "prefill"], default="all",
                     help="codec: only the codec decoder measurement (a 1-layer engine), "
-                         "printed as {\"codec\": ...}")
+                         "printed as {\"codec\": ...}; prompt: only the 256-token prompt "
+                         "(26 layers), printed as {\"prompt\": ...}; prefill: the same "
+                         "without its decode steps")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the frame loop runs on a single MI355X "
@@ -221,6 +226,12 @@ def main():
         eng = V.VoxtralEngine(V.default_config(n_layers=1), max_seq_len=64).init()
         eng.init_synthetic(0, 0.02)
         print(json.dumps({"codec": measure_codec(eng)}), flush=True)
+        eng.destroy()
+        return
+    if args.section in ("prompt", "prefill"):
+        eng = V.VoxtralEngine(V.default_config(), max_seq_len=4096).init()
+        eng.init_synthetic(0, 0.02)
+        print(json.dumps({"prompt": measure_prompt(eng, decode=args.section == "prompt")}), flush=True)
         eng.destroy()
         return
     t0 = time.time()

@@ -22,6 +22,7 @@
 #include "vx_prefill.h"
 #include "vx_codec.h"
 #include "vx_blas.h"
+#include "vx_gemm.h"
 #include "vx_loader.h"
 #include "vx_tokenizer.h"
 
@@ -154,6 +155,8 @@ struct vx_engine {
   // first use
   BlasGemm blas;
   bool blas_ready = false;
+  bool gemm_ready = false;
+  int cus = 0;  // compute units (prefill GEMM grids)
 
   void weights_changed() {
     tproj_ready = false;
@@ -1468,6 +1471,34 @@ static int blas_setup(vx_engine *e) {
   return VX_OK;
 }
 
+// The prefill GEMMs (vx_gemm.h): 144 KB of dynamic LDS per block and the
+// device's compute-unit count for the grids.
+static int pf_gemm_setup(vx_engine *e) {
+  if (e->gemm_ready) return VX_OK;
+  HIPCHK(e, gemm_setup());
+  int dev = 0;
+  HIPCHK(e, hipGetDevice(&dev));
+  HIPCHK(e, hipDeviceGetAttribute(&e->cus, hipDeviceAttributeMultiprocessorCount, dev));
+  if (e->cus < 8) return fail(e, VX_E_DEVICE, "unexpected compute unit count %d", e->cus);
+  e->gemm_ready = true;
+  return VX_OK;
+}
+
+// pf_c[s][col][m] for s < *ns: the ns K-slice partial sums of
+// W[M][K] x pf_b (2 nt rows of K halves)
+static int pf_gemm(vx_engine *e, const uint16_t *W, int M, int K, int nt, int *ns) {
+  if (M % GM_BM || K % GM_BK || nt % GM_BN)
+    return fail(e, VX_E_STATE, "prefill GEMM shape M %d K %d nt %d", M, K, nt);
+  const GemmPlan p = gemm_plan(M, K, nt, e->cus);
+  if (p.slices != 1 && p.slices != 2 && p.slices != 4 && p.slices != 8)
+    return fail(e, VX_E_STATE, "prefill GEMM plan with %d slices", p.slices);
+  if ((size_t)p.slices * nt * M > (size_t)PF_NC * 2 * HID)
+    return fail(e, VX_E_STATE, "prefill GEMM output (%d slices of %d x %d) exceeds its buffer", p.slices, nt, M);
+  gemm_launch(p, e->st, W, M, K, (const uint16_t *)e->pf_b, nt, e->pf_c);
+  *ns = p.slices;
+  return VX_OK;
+}
+
 // C[n][m] = sum_k W[m][k] B[n][k] on the engine's stream
 static int blas_gemm(vx_engine *e, const uint16_t *W, int M, int K, const h8 *B, int N, float *C) {
   const std::string err = e->blas.gemm(W, M, K, (const uint16_t *)B, N, C, e->st);
@@ -1477,8 +1508,8 @@ static int blas_gemm(vx_engine *e, const uint16_t *W, int M, int K, const h8 *B,
 
 static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int vcount,
                                  bool has_voice) {
-  int rc = VX_OK;
-  const int nt = pf_nt(n), N = 2 * nt;
+  int rc = VX_OK, ns = 1;
+  const int nt = pf_nt(n);
   hipStream_t st = e->st;
   const int pos0 = e->host_pos;
   hipLaunchKernelGGL(pf_embed_kernel, dim3(n, DIM / 256), dim3(256), 0, st, e->tok_emb, e->pf_tok,
@@ -1490,9 +1521,11 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
   for (int l = 0; l < e->cfg.n_layers; l++) {
     const LayerW &W = e->L[l];
     const bool next = l + 1 < e->cfg.n_layers;
-    if ((rc = blas_gemm(e, W.wqkv, QKV_ROWS, DIM, e->pf_b, N, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_qkv_epi_kernel, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c, nt,
-                       e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
+    if ((rc = pf_gemm(e, W.wqkv, QKV_ROWS, DIM, nt, &ns))) return rc;
+    pf_with_slices(ns, [&](auto NS) {
+      hipLaunchKernelGGL(pf_qkv_epi_kernel<NS>, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c, nt,
+                         e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
+    });
     if (e->kv_f32 && VX_PF_ATTN_MFMA)
       hipLaunchKernelGGL(pf_attn_mfma_kernel<float>, dim3(nt / PFA_T, NKV), blk, 0, st, e->pf_q,
                          (const float *)e->kc(l), (const float *)e->vc(l), e->max_seq, pos0, n, nt,
@@ -1507,20 +1540,26 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
     else
       hipLaunchKernelGGL(pf_attn_kernel<uint16_t>, dim3(nt, NKV), blk, 0, st, e->pf_q, e->kc(l),
                          e->vc(l), e->max_seq, pos0, n, nt, e->pf_b);
-    if ((rc = blas_gemm(e, W.wo, DIM, QD, e->pf_b, N, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_resid_pack_kernel<true>, dim3(nt), blk, 0, st, e->pf_c, n, nt, e->pf_x,
-                       W.ffn_norm, e->cfg.norm_eps, e->pf_b);
+    if ((rc = pf_gemm(e, W.wo, DIM, QD, nt, &ns))) return rc;
+    pf_with_slices(ns, [&](auto NS) {
+      hipLaunchKernelGGL((pf_resid_pack_kernel<true, NS>), dim3(nt), blk, 0, st, e->pf_c, n, nt, e->pf_x,
+                         W.ffn_norm, e->cfg.norm_eps, e->pf_b);
+    });
     // W1 and W3 are adjacent in the arena: one GEMM over the stacked rows
-    if ((rc = blas_gemm(e, W.w1, 2 * HID, DIM, e->pf_b, N, e->pf_c))) return rc;
-    hipLaunchKernelGGL(pf_swiglu_pack_kernel, dim3(nt, HID / 8 / 128), dim3(128), 0, st, e->pf_c,
-                       n, nt, e->pf_b);
-    if ((rc = blas_gemm(e, W.w2, DIM, HID, e->pf_b, N, e->pf_c))) return rc;
-    if (next)
-      hipLaunchKernelGGL(pf_resid_pack_kernel<true>, dim3(nt), blk, 0, st, e->pf_c, n, nt,
-                         e->pf_x, e->L[l + 1].attn_norm, e->cfg.norm_eps, e->pf_b);
-    else
-      hipLaunchKernelGGL(pf_resid_pack_kernel<false>, dim3(n), blk, 0, st, e->pf_c, n, nt,
-                         e->pf_x, nullptr, 0.f, nullptr);
+    if ((rc = pf_gemm(e, W.w1, 2 * HID, DIM, nt, &ns))) return rc;
+    pf_with_slices(ns, [&](auto NS) {
+      hipLaunchKernelGGL(pf_swiglu_pack_kernel<NS>, dim3(nt, HID / 8 / 128), dim3(128), 0, st, e->pf_c, n,
+                         nt, e->pf_b);
+    });
+    if ((rc = pf_gemm(e, W.w2, DIM, HID, nt, &ns))) return rc;
+    pf_with_slices(ns, [&](auto NS) {
+      if (next)
+        hipLaunchKernelGGL((pf_resid_pack_kernel<true, NS>), dim3(nt), blk, 0, st, e->pf_c, n, nt, e->pf_x,
+                           e->L[l + 1].attn_norm, e->cfg.norm_eps, e->pf_b);
+      else
+        hipLaunchKernelGGL((pf_resid_pack_kernel<false, NS>), dim3(n), blk, 0, st, e->pf_c, n, nt, e->pf_x,
+                           nullptr, 0.f, nullptr);
+    });
   }
   (void)hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * DIM, DIM * 4, hipMemcpyDeviceToDevice, st);
   hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, e->x, e->final_norm,
@@ -1545,7 +1584,7 @@ int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t au
       return fail(e, VX_E_INVALID, "token %d out of range", tokens[i]);
   if (e->L[0].w3 != e->L[0].w1 + (size_t)HID * DIM)
     return fail(e, VX_E_STATE, "weight layout: gate and up matrices not adjacent");
-  if ((rc = blas_setup(e))) return rc;
+  if ((rc = pf_gemm_setup(e))) return rc;
   const bool has_voice = voice && audio_count > 0;
   for (int c0 = 0; c0 < n_tokens; c0 += e->pf_chunk) {
     const int n = std::min(e->pf_chunk, n_tokens - c0);

@@ -2,18 +2,20 @@
 // one token per backboneStep (src/engine.ts:2457-2472); here a chunk of up
 // to PF_MAXT prompt tokens goes through each layer at once, so every weight
 // is read once per chunk and the projections are GEMMs
-//   C[col][m] = sum_k W[m][k] * B[col][k]
-// (f16 x f16 -> f32 on the matrix cores, through hipBLASLt: vx_blas.h).  W
-// is the layer's f16 weight matrix (row-major, as loaded); B holds the
-// chunk's activations in hi/lo form (column t = f16(y_t), column nt + t =
-// f16(y_t - hi), each column's K halves contiguous), so the product keeps
-// f32 accuracy.  Small per-token kernels do RoPE + K/V writes and the causal
+//   C[s][col][m] = sum_{k in slice s} W[m][k] * (B[col][k] + B[nt + col][k])
+// (f16 x f16 -> f32 on the matrix cores: vx_gemm.h).  W is the layer's f16
+// weight matrix (row-major, as loaded); B holds the chunk's activations in
+// hi/lo form (column t = f16(y_t), column nt + t = f16(y_t - hi), each
+// column's K halves contiguous), so the product keeps f32 accuracy.  The
+// GEMM leaves ns partial sums over slices of K in ns consecutive [nt][ldc]
+// blocks of C, and the consumer adds them in order.  Small per-token kernels do RoPE + K/V writes and the causal
 // attention, and each of them, or a residual add + RMSNorm, or SwiGLU,
 // writes the next GEMM's B directly.  The
 // result (K/V cache rows, residual stream, final norm of the last token,
 // position) equals that of the per-token steps up to f32 summation order.
 #pragma once
 #include "vx_kernels.h"
+#include <type_traits>
 
 namespace vx {
 
@@ -23,9 +25,38 @@ constexpr int PF_NC = 2 * PF_MAXT;     // B columns (hi, lo), at most
 // lo columns: N = 2 nt GEMM columns.
 __host__ __device__ constexpr int pf_nt(int n) { return (n + 127) / 128 * 128; }
 
-// value of output (token t, row m): hi column plus lo column
+// value of output (token t, row m): the sum of the NS K-slice blocks, in order
+template <int NS>
 __device__ __forceinline__ float pf_c(const float *C, int ldc, int nt, int t, int m) {
-  return C[(size_t)t * ldc + m] + C[(size_t)(nt + t) * ldc + m];
+  float v[NS];
+#pragma unroll
+  for (int s = 0; s < NS; s++) v[s] = C[((size_t)s * nt + t) * ldc + m];
+  float y = v[0];
+#pragma unroll
+  for (int s = 1; s < NS; s++) y += v[s];
+  return y;
+}
+// four consecutive rows m .. m + 3 (m % 4 == 0)
+template <int NS>
+__device__ __forceinline__ f32x4 pf_c4(const float *C, int ldc, int nt, int t, int m) {
+  f32x4 v[NS];
+#pragma unroll
+  for (int s = 0; s < NS; s++) v[s] = *(const f32x4 *)(C + ((size_t)s * nt + t) * ldc + m);
+  f32x4 y = v[0];
+#pragma unroll
+  for (int s = 1; s < NS; s++) y += v[s];
+  return y;
+}
+// calls f(std::integral_constant<int, NS>) for ns in {1, 2, 4, 8}
+template <typename F>
+inline bool pf_with_slices(int ns, F &&f) {
+  switch (ns) {
+    case 1: f(std::integral_constant<int, 1>{}); return true;
+    case 2: f(std::integral_constant<int, 2>{}); return true;
+    case 4: f(std::integral_constant<int, 4>{}); return true;
+    case 8: f(std::integral_constant<int, 8>{}); return true;
+    default: return false;
+  }
 }
 
 // ------------------------------------------------------- per-token kernels
@@ -78,10 +109,11 @@ __global__ __launch_bounds__(256) void pf_pack_kernel(const float *X, int K, int
 // QKV outputs: interleaved rope of q and k at position pos0 + t
 // (src/shaders.ts:224-256), q -> Q[t][QD], k and v -> cache rows pos0 + t.
 // Grid: (n, QKV_ROWS / 2 / 256), one row pair per thread.
+template <int NS>
 __global__ void pf_qkv_epi_kernel(const float *C, int nt, float *Q, void *kc, void *vc, int kv_f32,
                                   int max_seq, int pos0, const float *inv_freq) {
   const int t = blockIdx.x, row = 2 * (blockIdx.y * blockDim.x + threadIdx.x);
-  const float y0 = pf_c(C, QKV_ROWS, nt, t, row), y1 = pf_c(C, QKV_ROWS, nt, t, row + 1);
+  const float y0 = pf_c<NS>(C, QKV_ROWS, nt, t, row), y1 = pf_c<NS>(C, QKV_ROWS, nt, t, row + 1);
   const int pos = pos0 + t;
   if (row < QD + KVD) {
     const float ang = (float)pos * inv_freq[(row & (HD - 1)) >> 1];
@@ -111,7 +143,7 @@ __device__ __forceinline__ void pf_put8(h8 *B, int K, int nt, int t, int kb, con
 // rmsNorm(X[t]) * g (src/shaders.ts:137-183); columns of tokens t >= n are
 // zero.  Grid: nt blocks (n without PACK) of 256; thread i owns the 8-value
 // groups i and i + 256 (DIM / 8 = 384 groups).
-template <bool PACK>
+template <bool PACK, int NS>
 __global__ __launch_bounds__(256) void pf_resid_pack_kernel(const float *C, int n, int nt, float *X,
                                                             const uint16_t *g, float eps, h8 *B) {
   constexpr int NG = DIM / 8, GPT = (NG + 255) / 256;
@@ -124,13 +156,11 @@ __global__ __launch_bounds__(256) void pf_resid_pack_kernel(const float *C, int 
       const int kb = tid + 256 * i;
       if (kb < NG) {
         float *x = X + (size_t)t * DIM + kb * 8;
-        const float *ch = C + (size_t)t * DIM + kb * 8, *cl = C + (size_t)(nt + t) * DIM + kb * 8;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-          const f32x4 xv = *(const f32x4 *)(x + 4 * h), a = *(const f32x4 *)(ch + 4 * h),
-                      b = *(const f32x4 *)(cl + 4 * h);
+          const f32x4 xv = *(const f32x4 *)(x + 4 * h), a = pf_c4<NS>(C, DIM, nt, t, kb * 8 + 4 * h);
 #pragma unroll
-          for (int e = 0; e < 4; e++) v[i][4 * h + e] = xv[e] + (a[e] + b[e]);
+          for (int e = 0; e < 4; e++) v[i][4 * h + e] = xv[e] + a[e];
           *(f32x4 *)(x + 4 * h) = f32x4{v[i][4 * h], v[i][4 * h + 1], v[i][4 * h + 2], v[i][4 * h + 3]};
         }
 #pragma unroll
@@ -163,21 +193,17 @@ __global__ __launch_bounds__(256) void pf_resid_pack_kernel(const float *C, int 
 // src/shaders.ts:483-501) written as the down GEMM's B (K = HID); columns of
 // tokens t >= n are zero.  Grid: (nt, HID / 8 / 128) of 128, one 8-value
 // group per thread.
+template <int NS>
 __global__ __launch_bounds__(128) void pf_swiglu_pack_kernel(const float *C, int n, int nt, h8 *B) {
   const int t = blockIdx.x, kb = blockIdx.y * 128 + threadIdx.x;
   float y[8];
   if (t < n) {
-    const size_t ld = 2 * HID;
-    const float *gh = C + (size_t)t * ld + kb * 8, *gl = C + (size_t)(nt + t) * ld + kb * 8;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      const f32x4 a = *(const f32x4 *)(gh + 4 * h), b = *(const f32x4 *)(gl + 4 * h);
-      const f32x4 c = *(const f32x4 *)(gh + HID + 4 * h), d = *(const f32x4 *)(gl + HID + 4 * h);
+      const f32x4 gt = pf_c4<NS>(C, 2 * HID, nt, t, kb * 8 + 4 * h);
+      const f32x4 up = pf_c4<NS>(C, 2 * HID, nt, t, HID + kb * 8 + 4 * h);
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float gt = a[e] + b[e], up = c[e] + d[e];
-        y[4 * h + e] = (gt / (1.0f + expf(-gt))) * up;
-      }
+      for (int e = 0; e < 4; e++) y[4 * h + e] = (gt[e] / (1.0f + expf(-gt[e]))) * up[e];
     }
   } else {
 #pragma unroll
