@@ -103,6 +103,8 @@ struct vx_engine {
   float *fm_seq = nullptr, *fm_q = nullptr, *fm_k = nullptr, *fm_v = nullptr, *fm_attn = nullptr,
         *fm_act = nullptr, *fm_llm_out = nullptr, *sem_logits = nullptr, *tproj = nullptr,
         *xh = nullptr, *vel = nullptr, *noise = nullptr, *time_embed = nullptr;
+  // the last FM layer's acoustic-projection partials per 12-row tile
+  float *ac_part = nullptr, *ac_ssq = nullptr;
   bool tproj_ready = false;
   // FM layer matrices in the MFMA A-operand order (pack_mfma_a_kernel), and
   // the packed inputs / sums of squares the FM GEMMs hand to each other
@@ -422,9 +424,9 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
                        greedy_code ? 8194 : 0, e->sem_code);
   }
   for (int s = 0; s < e->nsteps(); s++) {
-    FmStepArgs fa{e->xh,      e->vel, e->fm_in,        e->tproj + (size_t)s * DIM,
-                  e->fm_llm_out, e->fm_seq, s, alpha, dt, noise_src, e->fm_b_attn,
-                  e->FL[0].attn_norm, e->fm_ssq_attn};
+    FmStepArgs fa{e->xh,      e->vel,    e->ac_part, e->ac_ssq, e->fm_in,
+                  e->tproj + (size_t)s * DIM, e->fm_llm_out, e->fm_seq, s, alpha, dt, noise_src,
+                  e->fm_b_attn, e->FL[0].attn_norm, e->fm_ssq_attn};
     hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256), dim3(256), 0, st, fa);
     int nssq_attn = DIM / 256;  // partial sums written by the kernel above
     for (int l = 0; l < e->cfg.fm_layers; l++) {
@@ -478,19 +480,22 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
           a.Bn = e->fm_b_attn;
           a.gn = e->FL[l + 1].attn_norm;
           a.ssq_out = e->fm_ssq_attn;
+        } else {  // the velocity's final norm + acoustic projection, split per tile
+          a.acw = e->fm_ac;
+          a.acg = e->fm_norm;
+          a.ac_part = e->ac_part;
+          a.ac_ssq = e->ac_ssq;
         }
         FM_GEMM_DOWN(st, a, DIM);
         nssq_attn = DIM / FTR;
       }
     }
-    {  // final norm of position 0 of each branch -> acoustic_out -> vel[s]
-      GemvArgs a = gargs(e->fm_ac, e->fm_seq, 3 * DIM, e->vel + (size_t)s * 2 * NAC, NAC, NAC);
-      a.norm_w = e->fm_norm;
-      a.eps = 1e-5f;
-      launch_gemv<2, W4, 1, EPI_PLAIN, true, DIM, DIM>(st, a);
-    }
+    // the step's velocities (final norm of position 0 of each branch ->
+    // acoustic_out) are finished from the partials by the next step's input
+    // kernel, and for the last step by fm_finish
   }
-  hipLaunchKernelGGL(fm_finish_kernel, dim3(1), dim3(64), 0, st, e->xh, e->vel, e->nsteps() - 1,
+  hipLaunchKernelGGL(fm_finish_kernel, dim3(1), dim3(256), 0, st, e->xh, e->vel, e->ac_part, e->ac_ssq,
+                     e->nsteps() - 1,
                      alpha, dt, e->codes, e->cfg.acoustic_levels, e->frame);
 }
 
@@ -990,6 +995,8 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   aplace((void **)&e->tproj, (size_t)ns * DIM * 4);
   aplace((void **)&e->xh, (size_t)(ns + 1) * NAC * 4);
   aplace((void **)&e->vel, (size_t)ns * 2 * NAC * 4);
+  aplace((void **)&e->ac_part, (size_t)2 * NAC * SSQ_MAX * 4);
+  aplace((void **)&e->ac_ssq, (size_t)2 * SSQ_MAX * 4);
   aplace((void **)&e->noise, NAC * 4);
   aplace((void **)&e->time_embed, DIM * 4);
   aplace((void **)&e->inv_freq, HD / 2 * 4);

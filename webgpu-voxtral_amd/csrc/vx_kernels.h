@@ -63,6 +63,25 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
+// The same sum without the LDS crossbar: four DPP steps leave each row of 16
+// lanes holding its row sum (quad_perm xor 1, xor 2, half-row mirror, row
+// mirror), then the four row sums are read out and added in a fixed order.
+// Every lane gets the same value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  const int b = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
@@ -898,6 +917,12 @@ struct Gemm6Args {
   h8 *Bn;                  // optional: next GEMM's packed input from the new values
   const uint16_t *gn;      //   times these gains (null: none)
   float *ssq_out;          //   and their sums of squares, vector-major [FMV][SSQ_MAX]
+  // optional (EPI_RESID, the FM's last layer): this tile's share of the
+  // acoustic projection of position 0 of each CFG branch (vectors 0 and 3),
+  // ac_part[(b * NAC + o) * SSQ_MAX + tile] = sum over the tile's rows r of
+  // acw[o][r] * acg[r] * y_b[r], and ac_ssq[b * SSQ_MAX + tile] = sum y_b[r]^2
+  const uint16_t *acw, *acg;
+  float *ac_part, *ac_ssq;
 };
 
 // Block = RG row tiles x KS k-slices (one wave each); a wave streams its
@@ -945,6 +970,19 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
   if (kp == 0) {
     if (EPI == EPI_RESID) eres = *(const f32x4 *)(a.out + (size_t)ev * a.os + er);
     if (a.Bn && a.gn) egn = *(const uint2 *)(a.gn + er);
+  }
+  // the acoustic-projection epilogue's weights and gains (below): lane
+  // handles outputs idx = lane and lane + 64 < 2 NAC, each a 12-row slice
+  uint2 acwv[2][FTR / 4], acgv[FTR / 4];
+  if (EPI == EPI_RESID && a.ac_part && kp == 0) {
+#pragma unroll
+    for (int q = 0; q < FTR / 4; q++) acgv[q] = ((const uint2 *)(a.acg + row0))[q];
+#pragma unroll
+    for (int rep = 0; rep < 2; rep++) {
+      const int o = (lane + 64 * rep) % NAC;
+#pragma unroll
+      for (int q = 0; q < FTR / 4; q++) acwv[rep][q] = ((const uint2 *)(a.acw + (size_t)o * DIM + row0))[q];
+    }
   }
   u32x4 wb[P][TL];
   h8 bb[P];
@@ -1039,6 +1077,48 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
       }
       bpack_put4(a.Bn, v, r, z);
       if (a.ssq_out && lane < 16) a.ssq_out[v * SSQ_MAX + tile] = s2;
+    }
+  }
+  if (EPI == EPI_RESID && a.ac_part) {
+    // rows row0 .. row0 + FTR of vectors 0 and 3 through LDS, then lane
+    // (b, o) = (idx / NAC, idx % NAC), idx = lane and lane + 64, sums its row
+    // of the tile
+    __shared__ __attribute__((aligned(16))) float acy[RG][2][FTR];
+    if (live && (v == 0 || v == 3)) *(f32x4 *)&acy[rg][v / 3][4 * (lane >> 4)] = y;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // the LDS writes of this wave are done
+    float gv[FTR];
+#pragma unroll
+    for (int q = 0; q < FTR / 4; q++) {
+      const uint2 gg = acgv[q];
+      const h2 g01 = __builtin_bit_cast(h2, gg.x), g23 = __builtin_bit_cast(h2, gg.y);
+      gv[4 * q] = (float)g01.x;
+      gv[4 * q + 1] = (float)g01.y;
+      gv[4 * q + 2] = (float)g23.x;
+      gv[4 * q + 3] = (float)g23.y;
+    }
+#pragma unroll
+    for (int rep = 0; rep < 2; rep++) {
+      const int idx = lane + 64 * rep;
+      if (idx < 2 * NAC) {
+        const int b = idx / NAC;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < FTR / 4; q++) {
+          const uint2 ww = acwv[rep][q];
+          const h2 w01 = __builtin_bit_cast(h2, ww.x), w23 = __builtin_bit_cast(h2, ww.y);
+          sum = fmaf((float)w01.x * gv[4 * q], acy[rg][b][4 * q], sum);
+          sum = fmaf((float)w01.y * gv[4 * q + 1], acy[rg][b][4 * q + 1], sum);
+          sum = fmaf((float)w23.x * gv[4 * q + 2], acy[rg][b][4 * q + 2], sum);
+          sum = fmaf((float)w23.y * gv[4 * q + 3], acy[rg][b][4 * q + 3], sum);
+        }
+        a.ac_part[(size_t)idx * SSQ_MAX + tile] = sum;
+      }
+    }
+    if (lane < 2) {
+      float s2 = 0.f;
+#pragma unroll
+      for (int r = 0; r < FTR; r++) s2 = fmaf(acy[rg][lane][r], acy[rg][lane][r], s2);
+      a.ac_ssq[lane * SSQ_MAX + tile] = s2;
     }
   }
 }
@@ -1260,7 +1340,8 @@ __device__ __forceinline__ float cfg_euler(float x, float vc, float vu, float al
 
 struct FmStepArgs {
   float *xh;          // x_t history [nfe][NAC]; row s is the input of step s
-  const float *vel;   // velocity history [nfe-1][2][NAC]
+  float *vel;         // velocity history [nfe-1][2][NAC]: row s - 1 written here
+  const float *ac_part, *ac_ssq;  // the last FM layer's acoustic-projection partials
   const uint16_t *w_in;  // input_projection [DIM][NAC]
   const float *tproj;    // time projection of step s [DIM]
   const float *llm;      // llm projection [DIM]
@@ -1273,11 +1354,42 @@ struct FmStepArgs {
   float *ssq_out;        //   and sums of squares, vector-major [FMV][SSQ_MAX]
 };
 
+// The velocities of an Euler step (acoustic_codebook_output(RMSNorm(position
+// 0)) of both CFG branches, src/engine.ts:1210-1224) from the partial sums
+// the last FM layer's down GEMM leaves per 12-row tile: vs[b * NAC + o] =
+// rs_b * sum over tiles of ac_part, rs_b = 1 / sqrt(sum ac_ssq / DIM + eps).
+// Block of 256 threads; every thread calls it; vs is valid after the
+// barrier inside.
+__device__ __forceinline__ void fm_velocity(const float *ac_part, const float *ac_ssq, float *vs) {
+  static_assert(SSQ_MAX == 256 && DIM / FTR == SSQ_MAX, "one partial per tile, 4 per lane");
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  f32x4 q[2], p[(2 * NAC + 3) / 4];
+#pragma unroll
+  for (int b = 0; b < 2; b++) q[b] = *(const f32x4 *)(ac_ssq + b * SSQ_MAX + 4 * lane);
+#pragma unroll
+  for (int i = 0; i < (2 * NAC + 3) / 4; i++) {
+    const int idx = w + 4 * i;
+    p[i] = idx < 2 * NAC ? *(const f32x4 *)(ac_part + (size_t)idx * SSQ_MAX + 4 * lane) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float rs[2];
+#pragma unroll
+  for (int b = 0; b < 2; b++)
+    rs[b] = 1.0f / sqrtf(wave_sum_dpp((q[b][0] + q[b][1]) + (q[b][2] + q[b][3])) / (float)DIM + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < (2 * NAC + 3) / 4; i++) {
+    const int idx = w + 4 * i;
+    const float sum = wave_sum_dpp((p[i][0] + p[i][1]) + (p[i][2] + p[i][3]));
+    if (idx < 2 * NAC && lane == 0) vs[idx] = sum * rs[idx / NAC];
+  }
+  __syncthreads();
+}
+
 // Start of Euler step s: x_s (from x_{s-1} and the CFG velocity of step
 // s-1, or the noise at s=0), x_t_proj = input_projection(x_s), and both CFG
 // sequences [x_t_proj, time_proj, llm | 0] (src/engine.ts:1292-1349).
 __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
   __shared__ float xs[NAC];
+  __shared__ float vs[2 * NAC];
   const int t = threadIdx.x;
   const int row = blockIdx.x * 256 + t;  // grid covers DIM exactly
   // this row's input-projection weights, time/llm projections and gain do
@@ -1287,13 +1399,16 @@ __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
   for (int j = 0; j < NAC / 4; j++) wr[j] = ((const uint2 *)(a.w_in + (size_t)row * NAC))[j];
   const float tp = a.tproj[row], lp = a.llm[row];
   const float g = h2f(a.gn[row]);
+  if (a.step > 0) {
+    fm_velocity(a.ac_part, a.ac_ssq, vs);
+    if (blockIdx.x == 0 && t < 2 * NAC) a.vel[(size_t)(a.step - 1) * 2 * NAC + t] = vs[t];
+  }
   if (t < NAC) {
     float x;
     if (a.step == 0) {
       x = a.noise[t];
     } else {
-      const float *vp = a.vel + (size_t)(a.step - 1) * 2 * NAC;
-      x = cfg_euler(a.xh[(a.step - 1) * NAC + t], vp[t], vp[NAC + t], a.alpha, a.dt);
+      x = cfg_euler(a.xh[(a.step - 1) * NAC + t], vs[t], vs[NAC + t], a.alpha, a.dt);
     }
     xs[t] = x;
     if (blockIdx.x == 0) a.xh[a.step * NAC + t] = x;
@@ -1361,12 +1476,15 @@ __global__ __launch_bounds__(64) void fm_attn_kernel(const float *q, const float
 // End of the Euler loop: last CFG/Euler update, then fsqQuantize (round
 // half to even) into the device acoustic codes; also advances the frame
 // counter of the noise generator.
-__global__ void fm_finish_kernel(float *xh, const float *vel, int last, float alpha, float dt,
-                                 uint32_t *codes, int levels, int *frame_counter) {
+__global__ __launch_bounds__(256) void fm_finish_kernel(float *xh, float *vel, const float *ac_part,
+                                                       const float *ac_ssq, int last, float alpha, float dt,
+                                                       uint32_t *codes, int levels, int *frame_counter) {
+  __shared__ float vs[2 * NAC];
   const int t = threadIdx.x;
+  fm_velocity(ac_part, ac_ssq, vs);
+  if (t < 2 * NAC) vel[(size_t)last * 2 * NAC + t] = vs[t];
   if (t < NAC) {
-    const float *vp = vel + (size_t)last * 2 * NAC;
-    float x = cfg_euler(xh[last * NAC + t], vp[t], vp[NAC + t], alpha, dt);
+    float x = cfg_euler(xh[last * NAC + t], vs[t], vs[NAC + t], alpha, dt);
     xh[(last + 1) * NAC + t] = x;
     float c = fminf(fmaxf(x, -1.0f), 1.0f);
     float top = (float)(levels - 1);
