@@ -330,7 +330,7 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
       hipLaunchKernelGGL(attn_partial_kernel<float>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
     else
       hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->attn);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->pos, e->attn);
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
     GemvArgs a = gargs(W.wo, e->attn, QD, e->x, 0, DIM);

@@ -36,7 +36,22 @@ constexpr int HID = 9216;
 constexpr int QKV_ROWS = QD + 2 * KVD;  // 6144
 constexpr int NAC = 36;
 constexpr int SEMV = 8320;
-constexpr int ATTN_SPLITS = 32;  // split-K factor of the decode attention
+// Decode attention split over the key axis: ATTN_SPLITS blocks per KV head.
+// With ATTN_TILE_ALIGN a split takes whole tiles of 32 keys (so at short
+// context some splits have no keys), and with ATTN_LIVE_COMBINE the combine
+// reads only the splits that have keys.
+#ifndef VX_ATTN_SPLITS
+#define VX_ATTN_SPLITS 32
+#endif
+#ifndef VX_ATTN_TILE_ALIGN
+#define VX_ATTN_TILE_ALIGN 0
+#endif
+#ifndef VX_ATTN_LIVE_COMBINE
+#define VX_ATTN_LIVE_COMBINE 0
+#endif
+constexpr int ATTN_SPLITS = VX_ATTN_SPLITS;
+constexpr bool ATTN_TILE_ALIGN = VX_ATTN_TILE_ALIGN != 0;
+constexpr bool ATTN_LIVE_COMBINE = VX_ATTN_LIVE_COMBINE != 0;
 static_assert(ATTN_SPLITS <= 64 && (ATTN_SPLITS & (ATTN_SPLITS - 1)) == 0, "splits: power of 2, <= 64");
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -530,6 +545,16 @@ struct AttnArgs {
 
 constexpr int AT_T = 32;  // keys per LDS tile
 
+// keys per split for seq keys: ceil(seq / ATTN_SPLITS), or (ATTN_TILE_ALIGN)
+// that many rounded up to whole tiles
+__device__ __forceinline__ int attn_chunk(int seq) {
+  if (ATTN_TILE_ALIGN) {
+    const int tiles = (seq + AT_T - 1) / AT_T;
+    return (tiles + ATTN_SPLITS - 1) / ATTN_SPLITS * AT_T;
+  }
+  return (seq + ATTN_SPLITS - 1) / ATTN_SPLITS;
+}
+
 // Geometry of one K or V tile of AT_T rows staged through LDS: 16-byte
 // chunks, CPT per thread (256 threads), rows padded by 16 bytes so that the
 // 32 lanes reading 32 different K rows at one column spread over the banks.
@@ -587,8 +612,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = kvh * (NH / NKV) + wave;
   const int seq = *a.pos + 1;
-  const int chunk = (seq + ATTN_SPLITS - 1) / ATTN_SPLITS;
-  const int p0 = split * chunk, p1 = min(seq, p0 + chunk);
+  const int chunk = attn_chunk(seq);
+  const int p0 = min(seq, split * chunk), p1 = min(seq, p0 + chunk);
   __shared__ __attribute__((aligned(16))) float qs[4][HD];
   __shared__ __attribute__((aligned(16))) KVT ks[AT_T * G::LDW];
   __shared__ __attribute__((aligned(16))) KVT vs[AT_T * G::LDW];
@@ -654,14 +679,22 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
 // o = sum o_s e^(m_s - M) / L (splits without keys carry m = -inf, l = 0).
 // Every load of the head (m, l of each split, both output dims of each
 // split) is issued before the first is used: one memory round trip.
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, float *out) {
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, const int *pos, float *out) {
   const int h = blockIdx.x, lane = threadIdx.x;
+  // splits with keys (ATTN_LIVE_COMBINE; the others hold m = -inf, l = 0)
+  int live = ATTN_SPLITS;
+  if (ATTN_LIVE_COMBINE) {
+    const int seq = *pos + 1, chunk = attn_chunk(seq);
+    live = (seq + chunk - 1) / chunk;
+  }
   const float *hp = part + (size_t)h * ATTN_SPLITS * (HD + 2);
   const float *mlp = hp + (lane & (ATTN_SPLITS - 1)) * (HD + 2) + HD;
-  const float mv = mlp[0], lv = mlp[1];
+  const bool lane_live = lane < ATTN_SPLITS && lane < live;
+  const float mv = lane_live ? mlp[0] : -INFINITY, lv = lane_live ? mlp[1] : 0.f;
   float2 o[ATTN_SPLITS];
 #pragma unroll
-  for (int s = 0; s < ATTN_SPLITS; s++) o[s] = *(const float2 *)(hp + s * (HD + 2) + lane * 2);
+  for (int s = 0; s < ATTN_SPLITS; s++)
+    o[s] = s < live ? *(const float2 *)(hp + s * (HD + 2) + lane * 2) : make_float2(0.f, 0.f);
   // keep every load ahead of the first use (one memory round trip)
   __builtin_amdgcn_sched_barrier(0);
   const float ms = lane < ATTN_SPLITS ? mv : -INFINITY;
