@@ -277,9 +277,22 @@ def main():
                  "frames_per_s": round(fps, 2), "x_realtime": round(fps * 0.08, 2),
                  "bytes_per_frame": fb,
                  "hbm_frac": round(fb * fps / 1e9 / HBM_PEAK_GBPS, 4),
-                 "sampling": "greedy masked argmax on device, no EOS"}
+                 "sampling": "greedy masked argmax on device, no EOS",
+                 "launches_per_euler_step": 16}
         log(f"[gpu] frame loop {fms / args.frames * 1000:.1f} us/frame -> {fps:.1f} frames/s "
             f"= {fps * 0.08:.1f}x real-time")
+
+    # ---- the flow-matching kernels one by one (after the frame loop, on the
+    # buffers a frame leaves), cycling over the 3 FM layers
+    fm_kern = None
+    if not args.no_frames:
+        fm_kern = {}
+        for k, name in enumerate(V.FM_KERNEL_NAMES):
+            us, b = eng.time_kernel(len(V.KERNEL_NAMES) + k, 63)
+            gbps = b / (us * 1e-6) / 1e9
+            fm_kern[name] = {"avg_us": round(us, 3), "bytes": b, "GBps": round(gbps, 1),
+                             "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+            log(f"[gpu] kernel {name:10s} {us:8.2f} us  {b / 1e6:8.2f} MB  {gbps:7.0f} GB/s")
 
     # ---- the 256-token prompt + 500 frame steps (the reference prefills per token)
     prompt = None
@@ -371,7 +384,7 @@ def main():
                      "frac": round(step_gbps / HBM_PEAK_GBPS, 4)},
         "roofline": roofline, "kernels": {k: {kk: round(vv, 3) for kk, vv in v.items()}
                                           for k, v in kern.items()},
-        "frame_loop": frame, "generate": gen, "prompt": prompt, "codec": codec,
+        "frame_loop": frame, "fm_kernels": fm_kern, "generate": gen, "prompt": prompt, "codec": codec,
         "long_context": long_ctx,
         "f16_kv_variant": f16kv,
         "cpu_baseline": cpu,

@@ -332,9 +332,18 @@ int vx_time_frames(vx_engine *e, int32_t n, float *ms);
 #define VX_KERNEL_OPROJ 2
 #define VX_KERNEL_GATEUP 3
 #define VX_KERNEL_DOWN 4
-/* Average duration of one launch of a backbone kernel (cycling over the
- * layers so no launch finds its weights in cache); *bytes = algorithmic
- * HBM bytes of one launch at the current position. */
+/* flow-matching kernels: the four MFMA GEMMs, the attention, the Euler
+ * step's input kernel */
+#define VX_KERNEL_FM_QKV 5
+#define VX_KERNEL_FM_ATTN 6
+#define VX_KERNEL_FM_O 7
+#define VX_KERNEL_FM_GATEUP 8
+#define VX_KERNEL_FM_DOWN 9
+#define VX_KERNEL_FM_STEP_IN 10
+/* Average duration of one launch of a backbone or FM kernel (cycling over
+ * the layers so no launch finds its weights in cache; FM kernels after one
+ * full FM pass, on the buffers it leaves); *bytes = algorithmic HBM bytes of
+ * one launch at the current position. */
 int vx_time_kernel(vx_engine *e, int32_t kernel, int32_t iters, float *avg_us,
                    double *bytes);
 

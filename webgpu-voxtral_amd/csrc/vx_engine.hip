@@ -407,6 +407,92 @@ static int ensure_tproj(vx_engine *e) {
   return VX_OK;
 }
 
+// The FM kernels of one Euler step, by kind (also timed one by one).
+enum FmKernel { FMK_QKV, FMK_ATTN, FMK_O, FMK_GATEUP, FMK_DOWN };
+
+// Kernel k of FM layer l.  nssq_attn: partial sums of squares of the QKV
+// input (DIM / 256 from the step's input kernel for layer 0, DIM / FTR from
+// the previous layer's down GEMM).
+static void enqueue_fm_kernel(vx_engine *e, int l, int k, int nssq_attn) {
+  hipStream_t st = e->st;
+  const LayerW &W = e->FL[l], &P = e->FP[l];
+  const bool last = l + 1 == e->cfg.fm_layers;
+  switch (k) {
+    case FMK_QKV: {  // RMSNorm + QKV (no rope: src/engine.ts:1108)
+      Gemm6Args a{};
+      a.W = P.wqkv;
+      a.B = e->fm_b_attn;
+      a.ssq = e->fm_ssq_attn;
+      a.nssq = nssq_attn;
+      a.eps = 1e-5f;
+      a.out = e->fm_q;
+      a.out_k = e->fm_k;
+      a.out_v = e->fm_v;
+      FM_GEMM_QKV(st, a, QKV_ROWS);
+      break;
+    }
+    case FMK_ATTN:
+      hipLaunchKernelGGL(fm_attn_kernel, dim3(NH, 2), dim3(64), 0, st, e->fm_q, e->fm_k, e->fm_v,
+                         e->fm_attn, e->fm_b_o);
+      break;
+    case FMK_O: {  // O + residual; hands norm(x) * ffn gains to gate/up
+      Gemm6Args a{};
+      a.W = P.wo;
+      a.B = e->fm_b_o;
+      a.out = e->fm_seq;
+      a.os = DIM;
+      a.Bn = e->fm_b_ffn;
+      a.gn = W.ffn_norm;
+      a.ssq_out = e->fm_ssq_ffn;
+      FM_GEMM_O(st, a, DIM);
+      break;
+    }
+    case FMK_GATEUP: {  // RMSNorm + gate/up + SwiGLU; hands the activation to down
+      Gemm6Args a{};
+      a.W = P.w1;
+      a.W2 = P.w3;
+      a.B = e->fm_b_ffn;
+      a.ssq = e->fm_ssq_ffn;
+      a.nssq = DIM / FTR;
+      a.eps = 1e-5f;
+      a.out = e->fm_act;
+      a.os = HID;
+      a.Bn = e->fm_b_act;
+      FM_GEMM_GATEUP(st, a, HID);
+      break;
+    }
+    default: {  // down + residual; hands norm(x) * next attention gains to the next layer
+      Gemm6Args a{};
+      a.W = P.w2;
+      a.B = e->fm_b_act;
+      a.out = e->fm_seq;
+      a.os = DIM;
+      if (!last) {
+        a.Bn = e->fm_b_attn;
+        a.gn = e->FL[l + 1].attn_norm;
+        a.ssq_out = e->fm_ssq_attn;
+      } else {  // the velocity's final norm + acoustic projection, split per tile
+        a.acw = e->fm_ac;
+        a.acg = e->fm_norm;
+        a.ac_part = e->ac_part;
+        a.ac_ssq = e->ac_ssq;
+      }
+      FM_GEMM_DOWN(st, a, DIM);
+      break;
+    }
+  }
+}
+
+// Start of Euler step s (x_s, the input projection, both CFG sequences).
+static void enqueue_fm_step_in(vx_engine *e, int s, const float *noise_src) {
+  const float alpha = e->cfg.cfg_alpha;
+  const float dt = (float)(1.0 / (double)(e->cfg.nfe - 1));
+  FmStepArgs fa{e->xh,      e->vel,    e->ac_part, e->ac_ssq, e->fm_in,
+                e->tproj + (size_t)s * DIM, e->fm_llm_out, e->fm_seq, s, alpha, dt, noise_src,
+                e->fm_b_attn, e->FL[0].attn_norm, e->fm_ssq_attn};
+  hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256), dim3(256), 0, e->st, fa);
+}
+
 // fmForward with CFG batched: 6 vectors (2 branches x 3 positions) share
 // every weight read; time projections come from the precomputed table.
 // noise_src: device f32[36] holding x_0.
@@ -424,79 +510,15 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
                        greedy_code ? 8194 : 0, e->sem_code);
   }
   for (int s = 0; s < e->nsteps(); s++) {
-    FmStepArgs fa{e->xh,      e->vel,    e->ac_part, e->ac_ssq, e->fm_in,
-                  e->tproj + (size_t)s * DIM, e->fm_llm_out, e->fm_seq, s, alpha, dt, noise_src,
-                  e->fm_b_attn, e->FL[0].attn_norm, e->fm_ssq_attn};
-    hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256), dim3(256), 0, st, fa);
-    int nssq_attn = DIM / 256;  // partial sums written by the kernel above
-    for (int l = 0; l < e->cfg.fm_layers; l++) {
-      const LayerW &W = e->FL[l], &P = e->FP[l];
-      const bool last = l + 1 == e->cfg.fm_layers;
-      {  // RMSNorm + QKV (no rope: src/engine.ts:1108)
-        Gemm6Args a{};
-        a.W = P.wqkv;
-        a.B = e->fm_b_attn;
-        a.ssq = e->fm_ssq_attn;
-        a.nssq = nssq_attn;
-        a.eps = 1e-5f;
-        a.out = e->fm_q;
-        a.out_k = e->fm_k;
-        a.out_v = e->fm_v;
-        FM_GEMM_QKV(st, a, QKV_ROWS);
-      }
-      hipLaunchKernelGGL(fm_attn_kernel, dim3(NH, 2), dim3(64), 0, st, e->fm_q, e->fm_k, e->fm_v,
-                         e->fm_attn, e->fm_b_o);
-      {  // O + residual; hands norm(x) * ffn gains to gate/up
-        Gemm6Args a{};
-        a.W = P.wo;
-        a.B = e->fm_b_o;
-        a.out = e->fm_seq;
-        a.os = DIM;
-        a.Bn = e->fm_b_ffn;
-        a.gn = W.ffn_norm;
-        a.ssq_out = e->fm_ssq_ffn;
-        FM_GEMM_O(st, a, DIM);
-      }
-      {  // RMSNorm + gate/up + SwiGLU; hands the activation to down
-        Gemm6Args a{};
-        a.W = P.w1;
-        a.W2 = P.w3;
-        a.B = e->fm_b_ffn;
-        a.ssq = e->fm_ssq_ffn;
-        a.nssq = DIM / FTR;
-        a.eps = 1e-5f;
-        a.out = e->fm_act;
-        a.os = HID;
-        a.Bn = e->fm_b_act;
-        FM_GEMM_GATEUP(st, a, HID);
-      }
-      {  // down + residual; hands norm(x) * next attention gains to the next layer
-        Gemm6Args a{};
-        a.W = P.w2;
-        a.B = e->fm_b_act;
-        a.out = e->fm_seq;
-        a.os = DIM;
-        if (!last) {
-          a.Bn = e->fm_b_attn;
-          a.gn = e->FL[l + 1].attn_norm;
-          a.ssq_out = e->fm_ssq_attn;
-        } else {  // the velocity's final norm + acoustic projection, split per tile
-          a.acw = e->fm_ac;
-          a.acg = e->fm_norm;
-          a.ac_part = e->ac_part;
-          a.ac_ssq = e->ac_ssq;
-        }
-        FM_GEMM_DOWN(st, a, DIM);
-        nssq_attn = DIM / FTR;
-      }
-    }
+    enqueue_fm_step_in(e, s, noise_src);
+    for (int l = 0; l < e->cfg.fm_layers; l++)
+      for (int k = FMK_QKV; k <= FMK_DOWN; k++) enqueue_fm_kernel(e, l, k, l == 0 ? DIM / 256 : DIM / FTR);
     // the step's velocities (final norm of position 0 of each branch ->
     // acoustic_out) are finished from the partials by the next step's input
     // kernel, and for the last step by fm_finish
   }
   hipLaunchKernelGGL(fm_finish_kernel, dim3(1), dim3(256), 0, st, e->xh, e->vel, e->ac_part, e->ac_ssq,
-                     e->nsteps() - 1,
-                     alpha, dt, e->codes, e->cfg.acoustic_levels, e->frame);
+                     e->nsteps() - 1, alpha, dt, e->codes, e->cfg.acoustic_levels, e->frame);
 }
 
 // ------------------------------------------------------------------ graphs
@@ -2197,9 +2219,40 @@ int vx_time_frames(vx_engine *e, int32_t n, float *out_ms) {
 }
 
 int vx_time_kernel(vx_engine *e, int32_t kernel, int32_t iters, float *avg_us, double *bytes) {
-  if (!e || iters < 1 || !avg_us || kernel < 0 || kernel > VX_KERNEL_DOWN) return VX_E_INVALID;
+  if (!e || iters < 1 || !avg_us || kernel < 0 || kernel > VX_KERNEL_FM_STEP_IN) return VX_E_INVALID;
   int rc = check_ready(e);
   if (rc) return rc;
+  if (kernel >= VX_KERNEL_FM_QKV) {
+    // one full FM pass first, so every FM buffer holds the values a frame has
+    if ((rc = ensure_tproj(e))) return rc;
+    enqueue_fm(e, e->noise, true);
+    const double fm_b[] = {
+        (double)QKV_ROWS * DIM * 2 + DIM * BCOL * 2 + 6.0 * QKV_ROWS * 4,
+        6.0 * (QD + 2 * KVD) * 4 + 6.0 * QD * 4 + QD * BCOL * 2,
+        (double)DIM * QD * 2 + QD * BCOL * 2 + 6.0 * DIM * 8 + DIM * BCOL * 2,
+        2.0 * HID * DIM * 2 + DIM * BCOL * 2 + 6.0 * HID * 4 + HID * BCOL * 2,
+        (double)DIM * HID * 2 + HID * BCOL * 2 + 6.0 * DIM * 8 + DIM * BCOL * 2,
+        (double)DIM * NAC * 2 + 2.0 * NAC * SSQ_MAX * 4 + 6.0 * DIM * 4 + DIM * BCOL * 2 + 2.0 * DIM * 4,
+    };
+    const int k = kernel - VX_KERNEL_FM_QKV;
+    if (bytes) *bytes = fm_b[k];
+    auto launch = [&](int i) {
+      const int l = i % e->cfg.fm_layers;
+      const int ns = e->nsteps();  // steps >= 1 read the previous step's partials
+      if (k == 5) enqueue_fm_step_in(e, ns > 1 ? 1 + i % (ns - 1) : 0, e->noise);
+      else enqueue_fm_kernel(e, l, k, l == 0 ? DIM / 256 : DIM / FTR);
+    };
+    for (int i = 0; i < 2; i++) launch(i);  // warm-up
+    HIPCHK(e, hipEventRecord(e->ev0, e->st));
+    for (int i = 0; i < iters; i++) launch(i);
+    HIPCHK(e, hipEventRecord(e->ev1, e->st));
+    LAUNCHCHK(e);
+    HIPCHK(e, hipEventSynchronize(e->ev1));
+    float ms;
+    HIPCHK(e, hipEventElapsedTime(&ms, e->ev0, e->ev1));
+    *avg_us = ms * 1000.0f / iters;
+    return VX_OK;
+  }
   if (e->host_pos >= e->max_seq)
     return fail(e, VX_E_RANGE, "position %d reaches max_seq_len %d", e->host_pos, e->max_seq);
   const double seq = (double)e->host_pos + 1.0;

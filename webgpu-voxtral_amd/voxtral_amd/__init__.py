@@ -22,6 +22,8 @@ EMBED_TOKEN, EMBED_AUDIO, EMBED_PRECOMPUTED, EMBED_CODES = 0, 1, 2, 3
 SAMPLE_TOP_P, SAMPLE_GREEDY, SAMPLE_TOP_P_HOST = 0, 1, 2
 KERNEL_QKV, KERNEL_ATTN, KERNEL_OPROJ, KERNEL_GATEUP, KERNEL_DOWN = range(5)
 KERNEL_NAMES = ["qkv", "attn", "oproj", "gateup", "down"]
+# flow-matching kernels, time_kernel indices 5.. (VX_KERNEL_FM_*)
+FM_KERNEL_NAMES = ["fm_qkv", "fm_attn", "fm_o", "fm_gateup", "fm_down", "fm_step_in"]
 
 
 class VoxtralError(RuntimeError):
