@@ -55,6 +55,8 @@ def lib():
             "vxo_splitmix64_next": (c_u64, [ctypes.POINTER(c_u64)]),
             "vxo_name_stream": (c_u64, [ctypes.c_char_p]),
             "vxo_normal": (c_float, [c_u64, c_u64, c_u64]),
+            "vxo_gauss": (c_float, [c_u64, c_u64, c_u64]),
+            "vxo_gen_gauss_f32": (None, [c_u64, c_u64, c_size, F32]),
             "vxo_gen_f32": (None, [c_u64, c_u64, c_size, c_float, c_float, F32]),
             "vxo_gen_f16": (None, [c_u64, c_u64, c_size, c_float, c_float, U16]),
             "vxo_matvec_f16": (None, [U16, F32, F32, c_int, c_int]),
@@ -139,6 +141,13 @@ def default_config(**over):
 # ---------------------------------------------------------------- numbers
 def name_stream(name):
     return lib().vxo_name_stream(name.encode())
+
+
+def gen_gauss_f32(seed, name, n):
+    """n Box-Muller Gaussians of (seed, stream(name)): the FM noise generator."""
+    out = np.empty(n, np.float32)
+    lib().vxo_gen_gauss_f32(seed, name_stream(name), n, out)
+    return out
 
 
 def gen_f32(seed, name, n, mean=0.0, std=1.0):

@@ -12,6 +12,9 @@
  *   splitmix64            published first outputs of the state-0 stream
  *   normal generator      exact integer Irwin-Hall sum recomputed in numpy;
  *                         moments; bit-identity with the GPU generator
+ *   FM noise (vxo_gauss)  Python restatement with exact fma, bit for bit;
+ *                         numpy Box-Muller in f64; moments and tails;
+ *                         bit-identity with the GPU generator
  *   matvec_f16            f64 numpy product (tolerance), and an explicit
  *                         restatement of the 256-lane strided/tree order
  *   rmsnorm               torch.nn.functional.rms_norm (f64)
@@ -165,6 +168,73 @@ float vxo_normal(uint64_t seed, uint64_t stream, uint64_t idx) {
   }
   int64_t zi = s - 6 * (int64_t)0xFFFFF;
   return (float)zi * 0x1p-20f;
+}
+
+/* Gaussian of (seed, stream, idx) by the Box-Muller transform the reference
+ * uses for the FM noise (src/engine.ts:1264-1273: sqrt(-2 ln u1) cos(2 pi u2),
+ * u1, u2 uniform), from two counter-hashed uniforms: u1 = N 2^-53 in (0, 1]
+ * with N = (h1 >> 11) + 1, u2 = U 2^-53 in [0, 1) with U = h2 >> 11.  The
+ * logarithm and cosine are evaluated with IEEE double additions,
+ * multiplications, one division, one square root and explicit fused
+ * multiply-adds in a fixed order (no library transcendental), so the device
+ * generator gives the identical float:
+ *   ln u1 = (e - 53) ln 2 + ln m, N = m 2^e with m in [sqrt(1/2), sqrt(2)),
+ *           ln m = 2 (s + s^3 p(s^2)), s = (m - 1) / (m + 1), p the atanh
+ *           series 1/3 + s^2/5 + ... + s^14/17 (Horner);
+ *   cos(2 pi u2): quadrant q = U >> 51, x = (U mod 2^51) 2^-51 (pi/2),
+ *           cos x, sin x by their Taylor series to x^20 / x^21 (Horner),
+ *           then cos x, -sin x, -cos x, sin x for q = 0..3. */
+static const double BM_LOGC[8] = {0x1.5555555555555p-2, 0x1.999999999999ap-3, 0x1.2492492492492p-3,
+                                  0x1.c71c71c71c71cp-4, 0x1.745d1745d1746p-4, 0x1.3b13b13b13b14p-4,
+                                  0x1.1111111111111p-4, 0x1.e1e1e1e1e1e1ep-5};
+static const double BM_COSC[10] = {-0x1.0000000000000p-1, 0x1.5555555555555p-5,  -0x1.6c16c16c16c17p-10,
+                                   0x1.a01a01a01a01ap-16, -0x1.27e4fb7789f5cp-22, 0x1.1eed8eff8d898p-29,
+                                   -0x1.93974a8c07c9dp-37, 0x1.ae7f3e733b81fp-45, -0x1.6827863b97d97p-53,
+                                   0x1.e542ba4020225p-62};
+static const double BM_SINC[10] = {-0x1.5555555555555p-3, 0x1.1111111111111p-7,  -0x1.a01a01a01a01ap-13,
+                                   0x1.71de3a556c734p-19, -0x1.ae64567f544e4p-26, 0x1.6124613a86d09p-33,
+                                   -0x1.ae7f3e733b81fp-41, 0x1.952c77030ad4ap-49, -0x1.2f49b46814157p-57,
+                                   0x1.71b8ef6dcf572p-66};
+#define BM_LN2 0x1.62e42fefa39efp-1
+#define BM_PIO2 0x1.921fb54442d18p+0
+#define BM_SQRT2 0x1.6a09e667f3bcdp+0
+
+float vxo_gauss(uint64_t seed, uint64_t stream, uint64_t idx) {
+  const uint64_t s0 = mix64(seed) ^ stream;
+  const uint64_t h1 = mix64(s0 + (2 * idx + 1) * GOLDEN), h2 = mix64(s0 + (2 * idx + 2) * GOLDEN);
+  const double d = (double)((h1 >> 11) + 1); /* exact */
+  uint64_t bits;
+  memcpy(&bits, &d, 8);
+  int e = (int)((bits >> 52) & 0x7FF) - 1023;
+  const uint64_t mb = (bits & 0xFFFFFFFFFFFFFull) | 0x3FF0000000000000ull;
+  double m;
+  memcpy(&m, &mb, 8);
+  if (m > BM_SQRT2) {
+    m = m * 0.5;
+    e += 1;
+  }
+  const double s = (m - 1.0) / (m + 1.0), s2 = s * s;
+  double p = BM_LOGC[7];
+  for (int k = 6; k >= 0; k--) p = fma(s2, p, BM_LOGC[k]);
+  const double lm = 2.0 * fma(s * s2, p, s);
+  const double lu = fma((double)(e - 53), BM_LN2, lm);
+  const double r = sqrt(-2.0 * lu);
+  const uint64_t U = h2 >> 11;
+  const int q = (int)(U >> 51);
+  const double x = ((double)(U & ((1ull << 51) - 1)) * 0x1p-51) * BM_PIO2, x2 = x * x;
+  double c = BM_COSC[9], sn = BM_SINC[9];
+  for (int k = 8; k >= 0; k--) {
+    c = fma(x2, c, BM_COSC[k]);
+    sn = fma(x2, sn, BM_SINC[k]);
+  }
+  c = fma(x2, c, 1.0);
+  sn = fma(x * x2, sn, x);
+  const double cs = q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+  return (float)(r * cs);
+}
+
+void vxo_gen_gauss_f32(uint64_t seed, uint64_t stream, size_t n, float *out) {
+  for (size_t i = 0; i < n; i++) out[i] = vxo_gauss(seed, stream, (uint64_t)i);
 }
 
 void vxo_gen_f32(uint64_t seed, uint64_t stream, size_t n, float mean,
@@ -1048,7 +1118,7 @@ void vxo_fm_forward_batched(vxo_engine *e, const float *noise) {
  *     (:2556-2563), then the 256-lane tree argmax (greedy, in place of
  *     sampleTopP :2565, whose Math.random nothing can reproduce);
  *   EOS on a semantic code <= 1 (:2568-2570).
- * The FM noise of frame f is x_0[i] = vxo_normal(noise_seed, stream("fm.noise"),
+ * The FM noise of frame f is x_0[i] = vxo_gauss(noise_seed, stream("fm.noise"),
  * 36 f + i) (the debugNoise path, :1266).  Teacher forcing: with forced_sem
  * and forced_ac (n_forced frames), frame f's own codes are reported but the
  * state the next frame embeds is forced_*[f], and EOS is not taken for
@@ -1080,7 +1150,7 @@ int vxo_generate(vxo_engine *e, const int32_t *tokens, int n_tokens, int audio_s
   int frames = 0;
   for (int f = 0; f < max_frames; f++) {
     if (f > 0) vxo_backbone_step_codes(e);
-    for (int i = 0; i < na; i++) noise[i] = vxo_normal(noise_seed, stream, (uint64_t)f * na + i);
+    for (int i = 0; i < na; i++) noise[i] = vxo_gauss(noise_seed, stream, (uint64_t)f * na + i);
     vxo_fm_forward_batched(e, noise);
     memcpy(masked, e->semantic_logits, (size_t)sv * sizeof(float));
     masked[0] = -INFINITY;

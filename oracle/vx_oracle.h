@@ -55,6 +55,9 @@ uint64_t vxo_name_stream(const char *name); /* FNV-1a 64 of a tensor name */
  * taken from outputs 4*idx..4*idx+3 of the splitmix64 stream keyed by
  * (seed, stream); exact in f32, identical on any IEEE machine. */
 float vxo_normal(uint64_t seed, uint64_t stream, uint64_t idx);
+/* Box-Muller Gaussian (the FM noise), bit-identical to the device's */
+float vxo_gauss(uint64_t seed, uint64_t stream, uint64_t idx);
+void vxo_gen_gauss_f32(uint64_t seed, uint64_t stream, size_t n, float *out);
 void vxo_gen_f32(uint64_t seed, uint64_t stream, size_t n, float mean,
                  float std, float *out);
 void vxo_gen_f16(uint64_t seed, uint64_t stream, size_t n, float mean,

@@ -105,11 +105,11 @@ def test_device_noise_generator(pair):
     g.debug_write("normed", normed)
     codes = g.fm_step_and_read()
     x0 = g.debug_read("x_history", 36)
-    # seed 0, stream "fm.noise", frame 0
-    assert np.array_equal(x0, O.gen_f32(0, "fm.noise", 36))
+    # seed 0, stream "fm.noise", frame 0: the Box-Muller generator, bit for bit
+    assert np.array_equal(x0, O.gen_gauss_f32(0, "fm.noise", 36))
     g.debug_write("normed", normed)
     g.fm_step_and_read()
     x0b = g.debug_read("x_history", 36)
-    full = O.gen_f32(0, "fm.noise", 72)
+    full = O.gen_gauss_f32(0, "fm.noise", 72)
     assert np.array_equal(x0b, full[36:])
     assert codes.min() >= 2 and codes.max() <= 22

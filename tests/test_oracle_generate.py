@@ -6,7 +6,8 @@ src/engine.ts:2416-2585) on the CPU:
     kick through the text embedding, frame 0 FM only, later frames' multi-
     codebook embedding, the per-position FM dataflow of the reference
     (fmForward, not the batched one vxo_generate uses), index 0 and >= 8194
-    masked before the argmax, and the fm.noise stream at frame*36 + i;
+    masked before the argmax, and the Box-Muller fm.noise stream at
+    frame*36 + i;
   - voice rows equal to the [AUDIO] token's own embedding change nothing, so
     the splice covers exactly the audio span (shifting it by one position
     would replace the BEGIN_AUDIO or NEXT_AUDIO_TEXT embedding);
@@ -35,7 +36,7 @@ def prompt():
 
 
 def noise(f):
-    return O.gen_f32(SEED_NOISE, "fm.noise", 36 * (f + 1))[36 * f:]
+    return O.gen_gauss_f32(SEED_NOISE, "fm.noise", 36 * (f + 1))[36 * f:]
 
 
 def masked_argmax(logits):

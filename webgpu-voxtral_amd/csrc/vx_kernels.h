@@ -835,6 +835,61 @@ __device__ __forceinline__ float normal_variate(uint64_t seed, uint64_t stream, 
   return (float)(s - 6 * (int64_t)0xFFFFF) * 0x1p-20f;
 }
 
+// Box-Muller Gaussian of (seed, stream, idx), the FM noise (the reference's
+// sqrt(-2 ln u1) cos(2 pi u2), src/engine.ts:1264-1273), bit-identical to the
+// CPU generator: the same two hashed uniforms, and ln / cos by fixed
+// sequences of correctly rounded double operations (series, no library
+// transcendental):
+//   u1 = N 2^-53, N = (h1 >> 11) + 1 = m 2^e, m in [sqrt(1/2), sqrt(2)):
+//   ln u1 = (e - 53) ln 2 + 2 (s + s^3 p(s^2)), s = (m - 1) / (m + 1), p the
+//   atanh series to s^14 / 17; u2 = U 2^-53: quadrant U >> 51, x = (U mod
+//   2^51) 2^-51 pi / 2, cos x and sin x by Taylor series to x^20 / x^21.
+__device__ __forceinline__ float fm_gauss(uint64_t seed, uint64_t stream, uint64_t idx) {
+  constexpr double LOGC[8] = {0x1.5555555555555p-2, 0x1.999999999999ap-3, 0x1.2492492492492p-3,
+                              0x1.c71c71c71c71cp-4, 0x1.745d1745d1746p-4, 0x1.3b13b13b13b14p-4,
+                              0x1.1111111111111p-4, 0x1.e1e1e1e1e1e1ep-5};
+  constexpr double COSC[10] = {-0x1.0000000000000p-1, 0x1.5555555555555p-5,  -0x1.6c16c16c16c17p-10,
+                               0x1.a01a01a01a01ap-16, -0x1.27e4fb7789f5cp-22, 0x1.1eed8eff8d898p-29,
+                               -0x1.93974a8c07c9dp-37, 0x1.ae7f3e733b81fp-45, -0x1.6827863b97d97p-53,
+                               0x1.e542ba4020225p-62};
+  constexpr double SINC[10] = {-0x1.5555555555555p-3, 0x1.1111111111111p-7,  -0x1.a01a01a01a01ap-13,
+                               0x1.71de3a556c734p-19, -0x1.ae64567f544e4p-26, 0x1.6124613a86d09p-33,
+                               -0x1.ae7f3e733b81fp-41, 0x1.952c77030ad4ap-49, -0x1.2f49b46814157p-57,
+                               0x1.71b8ef6dcf572p-66};
+  const uint64_t s0 = mix64(seed) ^ stream;
+  const uint64_t h1 = mix64(s0 + (2 * idx + 1) * 0x9E3779B97F4A7C15ull);
+  const uint64_t h2 = mix64(s0 + (2 * idx + 2) * 0x9E3779B97F4A7C15ull);
+  const double d = (double)((h1 >> 11) + 1);  // exact
+  const uint64_t bits = __builtin_bit_cast(uint64_t, d);
+  int e = (int)((bits >> 52) & 0x7FF) - 1023;
+  double m = __builtin_bit_cast(double, (bits & 0xFFFFFFFFFFFFFull) | 0x3FF0000000000000ull);
+  if (m > 0x1.6a09e667f3bcdp+0) {
+    m = __dmul_rn(m, 0.5);
+    e += 1;
+  }
+  const double s = __ddiv_rn(__dsub_rn(m, 1.0), __dadd_rn(m, 1.0)), s2 = __dmul_rn(s, s);
+  double p = LOGC[7];
+#pragma unroll
+  for (int k = 6; k >= 0; k--) p = __fma_rn(s2, p, LOGC[k]);
+  const double lm = __dmul_rn(2.0, __fma_rn(__dmul_rn(s, s2), p, s));
+  const double lu = __fma_rn((double)(e - 53), 0x1.62e42fefa39efp-1, lm);
+  const double r = __dsqrt_rn(__dmul_rn(-2.0, lu));
+  const uint64_t U = h2 >> 11;
+  const int q = (int)(U >> 51);
+  const double x = __dmul_rn(__dmul_rn((double)(U & ((1ull << 51) - 1)), 0x1p-51), 0x1.921fb54442d18p+0);
+  const double x2 = __dmul_rn(x, x);
+  double c = COSC[9], sn = SINC[9];
+#pragma unroll
+  for (int k = 8; k >= 0; k--) {
+    c = __fma_rn(x2, c, COSC[k]);
+    sn = __fma_rn(x2, sn, SINC[k]);
+  }
+  c = __fma_rn(x2, c, 1.0);
+  sn = __fma_rn(__dmul_rn(x, x2), sn, x);
+  const double cs = q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+  return (float)__dmul_rn(r, cs);
+}
+
 __global__ void gen_f16_kernel(uint16_t *out, size_t n, uint64_t seed, uint64_t stream,
                                float mean, float std) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1527,11 +1582,11 @@ __global__ __launch_bounds__(256) void fm_finish_kernel(float *xh, float *vel, c
   if (t == 0 && frame_counter) *frame_counter += 1;
 }
 
-// Device noise: x_0[i] = normal(seed, stream, frame*36 + i)
+// Device noise: x_0[i] = fm_gauss(seed, stream, frame*36 + i)
 __global__ void fm_noise_kernel(float *noise, const uint64_t *seed, uint64_t stream,
                                 const int *frame_counter) {
   const int t = threadIdx.x;
-  if (t < NAC) noise[t] = normal_variate(*seed, stream, (uint64_t)(*frame_counter) * NAC + t);
+  if (t < NAC) noise[t] = fm_gauss(*seed, stream, (uint64_t)(*frame_counter) * NAC + t);
 }
 
 }  // namespace vx
