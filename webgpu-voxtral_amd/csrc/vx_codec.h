@@ -3,8 +3,11 @@
 // shaders of src/shaders.ts:817-1110, 1432-1868.
 //
 // Every projection and convolution is one f16 x f16 -> f32 GEMM on the
-// matrix cores (hipBLASLt, vx_blas.h): the f16 weights times the
-// activations in hi/lo f16 form, so products keep f32 accuracy.
+// matrix cores, the hand-written kernels of vx_gemm.h shared with the
+// prefill: the f16 weights times the activations in hi/lo f16 form, so
+// products keep f32 accuracy. A GEMM may leave its sum in up to 8 K-slice
+// partials; the epilogue kernels below (template parameter NS) add them in
+// slice order, so every result is bit-reproducible.
 //   - the causal convs become GEMMs over an im2col B (k-major: column t holds
 //     x[t - (k_size-1) + kk][ci] at k = kk * c_in + ci) with the weights
 //     reordered to match once after loading; their weight norm g/||w|| is
@@ -39,9 +42,17 @@ constexpr size_t CX_CCAP = (size_t)CX_NC * 2 * CHID;  // GEMM output floats
 constexpr float CX_NORM_EPS = 0.01f, CX_QK_EPS = 1e-6f;
 static_assert(CKIN % 32 == 0 && CKIN >= CIN * CK_IN, "input conv k padding");
 
-// output (token t, row m) of a chunk's GEMM: hi column plus lo column
+// output (token t, row m) of a chunk's GEMM: the sum of its NS K-slice
+// blocks [nc / 2][ldc] (vx_gemm.h), in order
+template <int NS>
 __device__ __forceinline__ float cx_val(const float *C, int ldc, int nc, int t, int m) {
-  return C[(size_t)t * ldc + m] + C[(size_t)((nc >> 1) + t) * ldc + m];
+  float v[NS];
+#pragma unroll
+  for (int s = 0; s < NS; s++) v[s] = C[((size_t)s * (nc >> 1) + t) * ldc + m];
+  float y = v[0];
+#pragma unroll
+  for (int s = 1; s < NS; s++) y += v[s];
+  return y;
 }
 
 // k group kb (8 halves) of columns t (hi) and nt + t (lo); kg = K / 8
@@ -147,39 +158,43 @@ __global__ __launch_bounds__(256) void cx_pack_out_kernel(const float *X, int t0
 // ----------------------------------------------------------- epilogues
 // out[(t0 + t) * ldo + m] = rs[m] * y (conv weight norm g / ||w|| per
 // output channel), m < mv.  Grid: (n, ceil(mv / 256)).
+template <int NS>
 __global__ void cx_scale_rows_epi_kernel(const float *C, int ldc, int nc, int t0, const float *rs,
                                          int mv, float *out, int ldo) {
   const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
-  if (m < mv) out[(size_t)(t0 + t) * ldo + m] = rs[m] * cx_val(C, ldc, nc, t, m);
+  if (m < mv) out[(size_t)(t0 + t) * ldo + m] = rs[m] * cx_val<NS>(C, ldc, nc, t, m);
 }
 
 // transposed conv output: step 2 (t0 + t) + r, channel co from row r * CD + co.
 // Grid: (n, 2 * CD / 256).
+template <int NS>
 __global__ void cx_up_epi_kernel(const float *C, int nc, int t0, float *out) {
   const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
   const int r = m / CD, co = m - r * CD;
-  out[(size_t)(2 * (t0 + t) + r) * CD + co] = cx_val(C, 2 * CD, nc, t, m);
+  out[(size_t)(2 * (t0 + t) + r) * CD + co] = cx_val<NS>(C, 2 * CD, nc, t, m);
 }
 
 // layer scale + residual (batchedLayerScale, src/shaders.ts:1755-1781):
 // X = y * scale + X.  Grid: (n, CD / 256).
+template <int NS>
 __global__ void cx_resid_epi_kernel(const float *C, int nc, int t0, const uint16_t *scale,
                                     float *X) {
   const int t = blockIdx.x, m = blockIdx.y * blockDim.x + threadIdx.x;
   float *x = X + (size_t)(t0 + t) * CD + m;
-  *x = cx_val(C, CD, nc, t, m) * h2f(scale[m]) + *x;
+  *x = cx_val<NS>(C, CD, nc, t, m) * h2f(scale[m]) + *x;
 }
 
 // q, k, v from the stacked projection, q and k RMS-normalised per head
 // (qkNorm, src/shaders.ts:1787-1830: weight [CNH * CHDIM] read at h * CHDIM).
 // One wave per (token, part, head); grid (n, 3 * CNH / 4) of 256.
+template <int NS>
 __global__ __launch_bounds__(256) void cx_qkv_epi_kernel(const float *C, int nc, int t0,
                                                          const uint16_t *qn, const uint16_t *kn,
                                                          float *Q, float *K, float *V) {
   const int t = blockIdx.x, gi = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int part = gi / CNH, h = gi - part * CNH, d = 2 * lane;
   const int m = part * CD + h * CHDIM + d;
-  float y0 = cx_val(C, 3 * CD, nc, t, m), y1 = cx_val(C, 3 * CD, nc, t, m + 1);
+  float y0 = cx_val<NS>(C, 3 * CD, nc, t, m), y1 = cx_val<NS>(C, 3 * CD, nc, t, m + 1);
   if (part < 2) {
     const float ss = wave_sum(y0 * y0 + y1 * y1);
     const float r = 1.0f / sqrtf(ss / (float)CHDIM + CX_QK_EPS);
@@ -194,6 +209,7 @@ __global__ __launch_bounds__(256) void cx_qkv_epi_kernel(const float *C, int nc,
 // SwiGLU of the stacked gate/up projection (batchedSwiGLU,
 // src/shaders.ts:1697-1716), written as the packed B of the down projection
 // (k = hidden unit).  Grid: (nt, CHID / 8 / 256) of 256; columns t >= n are 0.
+template <int NS>
 __global__ __launch_bounds__(256) void cx_swiglu_epi_kernel(const float *C, int nc, int n, h8 *B) {
   const int t = blockIdx.x, kb = blockIdx.y * 256 + threadIdx.x;
   float y[8];
@@ -202,7 +218,7 @@ __global__ __launch_bounds__(256) void cx_swiglu_epi_kernel(const float *C, int 
     float a = 0.f;
     if (t < n) {
       const int m = kb * 8 + e;
-      const float g = cx_val(C, 2 * CHID, nc, t, m), u = cx_val(C, 2 * CHID, nc, t, CHID + m);
+      const float g = cx_val<NS>(C, 2 * CHID, nc, t, m), u = cx_val<NS>(C, 2 * CHID, nc, t, CHID + m);
       a = g / (1.0f + expf(-g)) * u;
     }
     y[e] = a;

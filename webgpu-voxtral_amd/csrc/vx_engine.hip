@@ -21,7 +21,6 @@
 #include "vx_kernels.h"
 #include "vx_prefill.h"
 #include "vx_codec.h"
-#include "vx_blas.h"
 #include "vx_gemm.h"
 #include "vx_loader.h"
 #include "vx_tokenizer.h"
@@ -153,10 +152,6 @@ struct vx_engine {
   uint32_t *cx_sem = nullptr, *cx_ac = nullptr;
   int cx_chunk = CX_MAXT;  // tokens per codec GEMM chunk (multiple of 128)
 
-  // the plain GEMMs of the prefill and the codec (hipBLASLt), set up on
-  // first use
-  BlasGemm blas;
-  bool blas_ready = false;
   bool gemm_ready = false;
   int cus = 0;  // compute units (prefill GEMM grids)
 
@@ -1489,17 +1484,6 @@ int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos) {
 // rows are already on the device.  Afterwards the residual stream and
 // W.normed hold the last token's values and the position is advanced, as
 // after n single steps.
-static int blas_setup(vx_engine *e) {
-  if (e->blas_ready) return VX_OK;
-  // VX_BLAS_TUNE=1 times the library's candidates per GEMM shape (faster
-  // on some shapes, but the pick, and so the rounding, can vary per process)
-  const char *tune = getenv("VX_BLAS_TUNE");
-  const std::string err = e->blas.init(size_t(64) << 20, tune && atoi(tune) != 0);
-  if (!err.empty()) return fail(e, VX_E_DEVICE, "%s", err.c_str());
-  e->blas_ready = true;
-  return VX_OK;
-}
-
 // The prefill GEMMs (vx_gemm.h): 144 KB of dynamic LDS per block and the
 // device's compute-unit count for the grids.
 static int pf_gemm_setup(vx_engine *e) {
@@ -1528,10 +1512,19 @@ static int pf_gemm(vx_engine *e, const uint16_t *W, int M, int K, int nt, int *n
   return VX_OK;
 }
 
-// C[n][m] = sum_k W[m][k] B[n][k] on the engine's stream
-static int blas_gemm(vx_engine *e, const uint16_t *W, int M, int K, const h8 *B, int N, float *C) {
-  const std::string err = e->blas.gemm(W, M, K, (const uint16_t *)B, N, C, e->st);
-  if (!err.empty()) return fail(e, VX_E_DEVICE, "%s (M %d, K %d, N %d)", err.c_str(), M, K, N);
+// cx_c[s][col][m] for s < *ns: the codec chunk's K-slice partial sums of
+// W[M][K] x cx_b (nc = 2 nt rows of K halves)
+static int cx_gemm(vx_engine *e, const uint16_t *W, int M, int K, int nc, int *ns) {
+  const int nt = nc / 2;
+  if (M % GM_BM || K % GM_BK || nt % GM_BN)
+    return fail(e, VX_E_STATE, "codec GEMM shape M %d K %d nt %d", M, K, nt);
+  const GemmPlan p = gemm_plan(M, K, nt, e->cus);
+  if (p.slices != 1 && p.slices != 2 && p.slices != 4 && p.slices != 8)
+    return fail(e, VX_E_STATE, "codec GEMM plan with %d slices", p.slices);
+  if ((size_t)p.slices * nt * M > CX_CCAP)
+    return fail(e, VX_E_STATE, "codec GEMM output (%d slices of %d x %d) exceeds its buffer", p.slices, nt, M);
+  gemm_launch(p, e->st, W, M, K, (const uint16_t *)e->cx_b, nt, e->cx_c);
+  *ns = p.slices;
   return VX_OK;
 }
 
@@ -1551,7 +1544,7 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
     const LayerW &W = e->L[l];
     const bool next = l + 1 < e->cfg.n_layers;
     if ((rc = pf_gemm(e, W.wqkv, QKV_ROWS, DIM, nt, &ns))) return rc;
-    pf_with_slices(ns, [&](auto NS) {
+    gm_with_slices(ns, [&](auto NS) {
       hipLaunchKernelGGL(pf_qkv_epi_kernel<NS>, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c, nt,
                          e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
     });
@@ -1570,18 +1563,18 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
       hipLaunchKernelGGL(pf_attn_kernel<uint16_t>, dim3(nt, NKV), blk, 0, st, e->pf_q, e->kc(l),
                          e->vc(l), e->max_seq, pos0, n, nt, e->pf_b);
     if ((rc = pf_gemm(e, W.wo, DIM, QD, nt, &ns))) return rc;
-    pf_with_slices(ns, [&](auto NS) {
+    gm_with_slices(ns, [&](auto NS) {
       hipLaunchKernelGGL((pf_resid_pack_kernel<true, NS>), dim3(nt), blk, 0, st, e->pf_c, n, nt, e->pf_x,
                          W.ffn_norm, e->cfg.norm_eps, e->pf_b);
     });
     // W1 and W3 are adjacent in the arena: one GEMM over the stacked rows
     if ((rc = pf_gemm(e, W.w1, 2 * HID, DIM, nt, &ns))) return rc;
-    pf_with_slices(ns, [&](auto NS) {
+    gm_with_slices(ns, [&](auto NS) {
       hipLaunchKernelGGL(pf_swiglu_pack_kernel<NS>, dim3(nt, HID / 8 / 128), dim3(128), 0, st, e->pf_c, n,
                          nt, e->pf_b);
     });
     if ((rc = pf_gemm(e, W.w2, DIM, HID, nt, &ns))) return rc;
-    pf_with_slices(ns, [&](auto NS) {
+    gm_with_slices(ns, [&](auto NS) {
       if (next)
         hipLaunchKernelGGL((pf_resid_pack_kernel<true, NS>), dim3(nt), blk, 0, st, e->pf_c, n, nt, e->pf_x,
                            e->L[l + 1].attn_norm, e->cfg.norm_eps, e->pf_b);
@@ -1851,9 +1844,12 @@ static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *c
   chunks(T, [&](int t0, int n, int nc) {
     hipLaunchKernelGGL(cx_pack_in_kernel, dim3(nc / 2), dim3(128), 0, st, e->cx_cb, e->cx_sem,
                        e->cx_ac, levels, t0, n, nc, e->cx_b);
-    if (!rc) rc = blas_gemm(e, e->cx_ain, CD, CKIN, e->cx_b, nc, e->cx_c);
-    hipLaunchKernelGGL(cx_scale_rows_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, CD, nc, t0,
-                       e->cx_rs_in, CD, e->cx_x, CD);
+    int ns = 1;
+    if (!rc) rc = cx_gemm(e, e->cx_ain, CD, CKIN, nc, &ns);
+    gm_with_slices(ns, [&](auto NS) {
+      hipLaunchKernelGGL(cx_scale_rows_epi_kernel<NS>, dim3(n, CD / 256), blk, 0, st, e->cx_c, CD, nc, t0,
+                         e->cx_rs_in, CD, e->cx_x, CD);
+    });
   });
   int TT = T, at = VX_CODEC_STOP_INPUT_CONV;
   float *x = e->cx_x, *x2 = e->cx_x2;
@@ -1864,29 +1860,40 @@ static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *c
       chunks(TT, [&](int t0, int n, int nc) {
         hipLaunchKernelGGL(cx_pack_kernel<true>, dim3(nc / 2), blk, 0, st, x, CD, t0, n, nc,
                            L.attn_norm, CX_NORM_EPS, e->cx_b);
-        if (!rc) rc = blas_gemm(e, L.wqkv, 3 * CD, CD, e->cx_b, nc, e->cx_c);
-        hipLaunchKernelGGL(cx_qkv_epi_kernel, dim3(n, 3 * CNH / 4), blk, 0, st, e->cx_c, nc, t0,
-                           L.q_norm, L.k_norm, e->cx_q, e->cx_k, e->cx_v);
+        int ns = 1;
+        if (!rc) rc = cx_gemm(e, L.wqkv, 3 * CD, CD, nc, &ns);
+        gm_with_slices(ns, [&](auto NS) {
+          hipLaunchKernelGGL(cx_qkv_epi_kernel<NS>, dim3(n, 3 * CNH / 4), blk, 0, st, e->cx_c, nc, t0,
+                             L.q_norm, L.k_norm, e->cx_q, e->cx_k, e->cx_v);
+        });
       });
       hipLaunchKernelGGL(cx_attn_kernel, dim3(TT, CNH / 4), blk, 0, st, e->cx_q, e->cx_k, e->cx_v,
                          kWindow[s], e->cx_attn);
       chunks(TT, [&](int t0, int n, int nc) {
         hipLaunchKernelGGL(cx_pack_kernel<false>, dim3(nc / 2), blk, 0, st, e->cx_attn, CD, t0, n,
                            nc, nullptr, 0.f, e->cx_b);
-        if (!rc) rc = blas_gemm(e, L.wo, CD, CD, e->cx_b, nc, e->cx_c);
-        hipLaunchKernelGGL(cx_resid_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, t0,
-                           L.attn_scale, x);
+        int ns = 1;
+        if (!rc) rc = cx_gemm(e, L.wo, CD, CD, nc, &ns);
+        gm_with_slices(ns, [&](auto NS) {
+          hipLaunchKernelGGL(cx_resid_epi_kernel<NS>, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, t0,
+                             L.attn_scale, x);
+        });
       });
       chunks(TT, [&](int t0, int n, int nc) {
         hipLaunchKernelGGL(cx_pack_kernel<true>, dim3(nc / 2), blk, 0, st, x, CD, t0, n, nc,
                            L.ffn_norm, CX_NORM_EPS, e->cx_b);
-        if (!rc) rc = blas_gemm(e, L.w13, 2 * CHID, CD, e->cx_b, nc, e->cx_c);
+        int ns = 1;
+        if (!rc) rc = cx_gemm(e, L.w13, 2 * CHID, CD, nc, &ns);
         // the gate/up GEMM has consumed B: the SwiGLU epilogue refills it
-        hipLaunchKernelGGL(cx_swiglu_epi_kernel, dim3(nc / 2, CHID / 8 / 256), blk, 0, st, e->cx_c,
-                           nc, n, e->cx_b);
-        if (!rc) rc = blas_gemm(e, L.w2, CD, CHID, e->cx_b, nc, e->cx_c);
-        hipLaunchKernelGGL(cx_resid_epi_kernel, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, t0,
-                           L.ffn_scale, x);
+        gm_with_slices(ns, [&](auto NS) {
+          hipLaunchKernelGGL(cx_swiglu_epi_kernel<NS>, dim3(nc / 2, CHID / 8 / 256), blk, 0, st, e->cx_c,
+                             nc, n, e->cx_b);
+        });
+        if (!rc) rc = cx_gemm(e, L.w2, CD, CHID, nc, &ns);
+        gm_with_slices(ns, [&](auto NS) {
+          hipLaunchKernelGGL(cx_resid_epi_kernel<NS>, dim3(n, CD / 256), blk, 0, st, e->cx_c, nc, t0,
+                             L.ffn_scale, x);
+        });
       });
     }
     at = VX_CODEC_STOP_STAGE0 + 2 * s;
@@ -1895,8 +1902,11 @@ static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *c
     chunks(TT, [&](int t0, int n, int nc) {
       hipLaunchKernelGGL(cx_pack_up_kernel, dim3(nc / 2), blk, 0, st, x, e->cx_s_up[s], t0, n, nc,
                          e->cx_b);
-      if (!rc) rc = blas_gemm(e, e->cx_aup[s], 2 * CD, CKUP, e->cx_b, nc, e->cx_c);
-      hipLaunchKernelGGL(cx_up_epi_kernel, dim3(n, 2 * CD / 256), blk, 0, st, e->cx_c, nc, t0, x2);
+      int ns = 1;
+      if (!rc) rc = cx_gemm(e, e->cx_aup[s], 2 * CD, CKUP, nc, &ns);
+      gm_with_slices(ns, [&](auto NS) {
+        hipLaunchKernelGGL(cx_up_epi_kernel<NS>, dim3(n, 2 * CD / 256), blk, 0, st, e->cx_c, nc, t0, x2);
+      });
     });
     std::swap(x, x2);
     TT *= 2;
@@ -1912,9 +1922,12 @@ static int codec_run(vx_engine *e, int T, int stop, const float **res, size_t *c
   // [240 t, 240 t + 240)
   chunks(TT, [&](int t0, int n, int nc) {
     hipLaunchKernelGGL(cx_pack_out_kernel, dim3(nc / 2), blk, 0, st, x, t0, n, nc, e->cx_b);
-    if (!rc) rc = blas_gemm(e, e->cx_aout, CPATCH_ROWS, CKOUT, e->cx_b, nc, e->cx_c);
-    hipLaunchKernelGGL(cx_scale_rows_epi_kernel, dim3(n, 1), blk, 0, st, e->cx_c, CPATCH_ROWS, nc,
-                       t0, e->cx_rs_out, CPATCH, e->cx_audio, CPATCH);
+    int ns = 1;
+    if (!rc) rc = cx_gemm(e, e->cx_aout, CPATCH_ROWS, CKOUT, nc, &ns);
+    gm_with_slices(ns, [&](auto NS) {
+      hipLaunchKernelGGL(cx_scale_rows_epi_kernel<NS>, dim3(n, 1), blk, 0, st, e->cx_c, CPATCH_ROWS, nc,
+                         t0, e->cx_rs_out, CPATCH, e->cx_audio, CPATCH);
+    });
   });
   if (rc) return rc;
   *res = e->cx_audio;
@@ -1934,7 +1947,7 @@ static int codec_decode_impl(vx_engine *e, const uint32_t *semantic, const uint3
   if (out_count < vx_codec_stop_count(n_frames, stop))
     return fail(e, VX_E_INVALID, "output holds %zu floats, %zu needed", out_count,
                 vx_codec_stop_count(n_frames, stop));
-  if ((rc = codec_prepare(e)) || (rc = codec_reserve(e, n_frames)) || (rc = blas_setup(e)))
+  if ((rc = codec_prepare(e)) || (rc = codec_reserve(e, n_frames)) || (rc = pf_gemm_setup(e)))
     return rc;
   HIPCHK(e, hipMemcpyAsync(e->cx_sem, semantic, (size_t)n_frames * 4, hipMemcpyHostToDevice, e->st));
   HIPCHK(e, hipMemcpyAsync(e->cx_ac, acoustic, (size_t)n_frames * NAC * 4, hipMemcpyHostToDevice,

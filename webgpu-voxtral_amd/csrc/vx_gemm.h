@@ -366,6 +366,20 @@ struct GemmPlan {
   int slices = 1;  // C blocks the consumer sums
 };
 
+// Calls f(std::integral_constant<int, NS>) for the slice counts a plan can
+// produce (ns in {1, 2, 4, 8}), so the consumer kernels sum a compile-time
+// number of slices; false for any other count.
+template <typename F>
+inline bool gm_with_slices(int ns, F &&f) {
+  switch (ns) {
+    case 1: f(std::integral_constant<int, 1>{}); return true;
+    case 2: f(std::integral_constant<int, 2>{}); return true;
+    case 4: f(std::integral_constant<int, 4>{}); return true;
+    case 8: f(std::integral_constant<int, 8>{}); return true;
+    default: return false;
+  }
+}
+
 // cus: the device's compute units (8 XCDs).  Shapes must satisfy
 // M % 256 == 0, nt % 64 == 0, K % 64 == 0.
 inline GemmPlan gemm_plan(int M, int K, int nt, int cus) {

@@ -47,17 +47,6 @@ __device__ __forceinline__ f32x4 pf_c4(const float *C, int ldc, int nt, int t, i
   for (int s = 1; s < NS; s++) y += v[s];
   return y;
 }
-// calls f(std::integral_constant<int, NS>) for ns in {1, 2, 4, 8}
-template <typename F>
-inline bool pf_with_slices(int ns, F &&f) {
-  switch (ns) {
-    case 1: f(std::integral_constant<int, 1>{}); return true;
-    case 2: f(std::integral_constant<int, 2>{}); return true;
-    case 4: f(std::integral_constant<int, 4>{}); return true;
-    case 8: f(std::integral_constant<int, 8>{}); return true;
-    default: return false;
-  }
-}
 
 // ------------------------------------------------------- per-token kernels
 // X[t] = token embedding row, or voice row v = t + tok0 - vstart for the
