@@ -131,23 +131,28 @@ def measure_prompt(eng, reps=5, decode=True):
                     "back through W.normed as the precomputed embedding, HIP events"}
 
 
-def measure_codec(eng, T=250, reps=3):
-    """codecDecode of T frames of random codes, wall time per call."""
+def measure_codec(eng, T=250, reps=10, warm=3):
+    """codecDecode of T frames of random codes, wall time per call (median
+    of reps after warm calls)."""
     rng = np.random.default_rng(5)
     sem = rng.integers(2, 8194, T).astype(np.uint32)
     ac = rng.integers(2, 23, (T, 36)).astype(np.uint32)
-    eng.codec_decode(sem, ac)
-    t = time.perf_counter()
-    for _ in range(reps):
+    for _ in range(warm):
         eng.codec_decode(sem, ac)
-    cms = (time.perf_counter() - t) / reps * 1000.0
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        eng.codec_decode(sem, ac)
+        times.append(time.perf_counter() - t)
+    cms = float(np.median(times)) * 1000.0
     fl = codec_flops(T)
     codec = {"frames": T, "audio_s": T * 0.08, "ms": round(cms, 3),
              "x_realtime": round(T * 0.08 / (cms * 1e-3), 1),
              "algorithmic_GFLOP": round(fl / 1e9, 2),
              "TFLOPs": round(fl / (cms * 1e-3) / 1e12, 2),
              "mfma_issued_frac_of_peak": round(2 * fl / (cms * 1e-3) / 2.5e15, 4),
-             "note": "wall time per call incl. code upload and audio readback; "
+             "note": "wall time per call incl. code upload and audio readback, median of "
+                     f"{reps} after {warm} warm-up calls; "
                      "f16 weights x hi/lo f16 activations on MFMA (2 issued flops per "
                      "algorithmic flop)"}
     log(f"[gpu] codec decode {T} frames: {cms:.2f} ms = {codec['x_realtime']:.0f}x real-time, "

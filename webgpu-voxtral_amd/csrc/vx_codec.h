@@ -55,6 +55,46 @@ __device__ __forceinline__ float cx_val(const float *C, int ldc, int nc, int t, 
   return y;
 }
 
+// outputs m .. m + 7 (m % 8 == 0) of token t, the same in-order sums as
+// cx_val, from two 16-byte loads per K-slice block
+template <int NS>
+__device__ __forceinline__ void cx_val8(const float *C, int ldc, int nc, int t, int m, float (&y)[8]) {
+  f32x4 a[NS], b[NS];
+#pragma unroll
+  for (int s = 0; s < NS; s++) {
+    const float *p = C + ((size_t)s * (nc >> 1) + t) * ldc + m;
+    a[s] = *(const f32x4 *)p;
+    b[s] = *(const f32x4 *)(p + 4);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    y[e] = a[0][e];
+    y[4 + e] = b[0][e];
+  }
+#pragma unroll
+  for (int s = 1; s < NS; s++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      y[e] += a[s][e];
+      y[4 + e] += b[s][e];
+    }
+}
+
+// 8 consecutive f32 / f16 values from 16-byte aligned addresses
+__device__ __forceinline__ void cx_load8(const float *x, float (&y)[8]) {
+  const f32x4 a = *(const f32x4 *)x, b = *(const f32x4 *)(x + 4);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    y[e] = a[e];
+    y[4 + e] = b[e];
+  }
+}
+__device__ __forceinline__ void cx_load8h(const uint16_t *g, float (&y)[8]) {
+  const h8 w = *(const h8 *)g;
+#pragma unroll
+  for (int e = 0; e < 8; e++) y[e] = (float)w[e];
+}
+
 // k group kb (8 halves) of columns t (hi) and nt + t (lo); kg = K / 8
 __device__ __forceinline__ void cx_put(h8 *B, int nc, int kg, int kb, int t, const float (&y)[8]) {
   h8 hi, lo;
@@ -84,10 +124,17 @@ __global__ __launch_bounds__(256) void cx_pack_kernel(const float *X, int K, int
   }
   for (int kb = tid; kb < K / 8; kb += 256) {
     float y[8];
+    if (live) {
+      cx_load8(x + kb * 8, y);
+      if (NORM) {
+        float gv[8];
+        cx_load8h(g + kb * 8, gv);
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const int k = kb * 8 + e;
-      y[e] = live ? (NORM ? x[k] * r * h2f(g[k]) : x[k]) : 0.f;
+        for (int e = 0; e < 8; e++) y[e] = y[e] * r * gv[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) y[e] = 0.f;
     }
     cx_put(B, nc, K / 8, kb, t, y);
   }
@@ -134,8 +181,16 @@ __global__ __launch_bounds__(256) void cx_pack_up_kernel(const float *X, const f
     const int j = kb / (CD / 8), ci0 = (kb - j * (CD / 8)) * 8, src = tau - j;
     const bool ok = t < n && src >= 0;
     float y[8];
+    if (ok) {
+      float sc[8];
+      cx_load8(X + (size_t)src * CD + ci0, y);
+      cx_load8(scale + ci0, sc);
 #pragma unroll
-    for (int e = 0; e < 8; e++) y[e] = ok ? scale[ci0 + e] * X[(size_t)src * CD + ci0 + e] : 0.f;
+      for (int e = 0; e < 8; e++) y[e] = sc[e] * y[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) y[e] = 0.f;
+    }
     cx_put(B, nc, CKUP / 8, kb, t, y);
   }
 }
@@ -147,10 +202,13 @@ __global__ __launch_bounds__(256) void cx_pack_out_kernel(const float *X, int t0
   const int t = blockIdx.x, tau = t0 + t;
   for (int kb = threadIdx.x; kb < CKOUT / 8; kb += 256) {
     const int kk = kb / (CD / 8), ci0 = (kb - kk * (CD / 8)) * 8, src = tau - (CK_OUT - 1) + kk;
-    const bool ok = t < n && src >= 0;
     float y[8];
+    if (t < n && src >= 0) {
+      cx_load8(X + (size_t)src * CD + ci0, y);
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; e++) y[e] = ok ? X[(size_t)src * CD + ci0 + e] : 0.f;
+      for (int e = 0; e < 8; e++) y[e] = 0.f;
+    }
     cx_put(B, nc, CKOUT / 8, kb, t, y);
   }
 }
@@ -213,15 +271,15 @@ template <int NS>
 __global__ __launch_bounds__(256) void cx_swiglu_epi_kernel(const float *C, int nc, int n, h8 *B) {
   const int t = blockIdx.x, kb = blockIdx.y * 256 + threadIdx.x;
   float y[8];
+  if (t < n) {
+    float g[8], u[8];
+    cx_val8<NS>(C, 2 * CHID, nc, t, kb * 8, g);
+    cx_val8<NS>(C, 2 * CHID, nc, t, CHID + kb * 8, u);
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    float a = 0.f;
-    if (t < n) {
-      const int m = kb * 8 + e;
-      const float g = cx_val<NS>(C, 2 * CHID, nc, t, m), u = cx_val<NS>(C, 2 * CHID, nc, t, CHID + m);
-      a = g / (1.0f + expf(-g)) * u;
-    }
-    y[e] = a;
+    for (int e = 0; e < 8; e++) y[e] = g[e] / (1.0f + expf(-g[e])) * u[e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++) y[e] = 0.f;
   }
   cx_put(B, nc, CHID / 8, kb, t, y);
 }

@@ -26,8 +26,8 @@
 //    slices (S_out = KS); for shapes with at most one block per CU.
 //  - gemm_stream_kernel: one block per CU, each doing an equal share of the
 //    column tile's (row tile, k-tile) sequence, at most 2 blocks per tile
-//    (S_out = 2); for shapes with more tiles than CUs, which would otherwise
-//    run in uneven rounds.
+//    (S_out = 2, or 1 when the shares are whole tiles); for shapes with more
+//    tiles than CUs, which would otherwise run in uneven rounds.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <cstdint>
@@ -260,7 +260,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // sequence g = mt * nk + kt, g in [j L, (j + 1) L) with L >= nk, so a tile
 // is done by at most two blocks.  The part of a tile that starts at kt = 0
 // goes to C block 0, the other part to block 1; a tile done by one block
-// writes zeros to block 1.  The n_tiles blocks of a share read the same
+// writes zeros to block 1, unless every share is whole tiles (then only
+// block 0 is written and the consumer reads one slice).  The n_tiles blocks of a share read the same
 // weight k-tiles at the same time; XCD x (blocks b with b % 8 == x) holds
 // whole shares, so one L2 serves them.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stream_kernel(
@@ -276,6 +277,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int g0 = min(j * Lshare, total), g1 = min(g0 + Lshare, total);
   if (g0 >= g1) return;
   const int last = g1 - 1;
+  // shares of whole tiles: every tile is done by one block, C block 1 unused
+  const bool whole = Lshare % nk == 0;
   // per-lane offsets of the direct loads from the k-tile's weight / B origin
   size_t off[GM_LOADS];
 #pragma unroll
@@ -334,7 +337,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if (end_tile || g == last) {
       gm_store(L, acc, C + (seg_k0 == 0 ? 0 : (size_t)nt * ldc), ldc, c * GM_BN, c_mt * GM_BM, false);
       stored = 16;
-      if (seg_k0 == 0 && end_tile) {
+      if (seg_k0 == 0 && end_tile && !whole) {
         gm_store(L, acc, C + (size_t)nt * ldc, ldc, c * GM_BN, c_mt * GM_BM, true);
         stored = 32;
       }
@@ -391,7 +394,7 @@ inline GemmPlan gemm_plan(int M, int K, int nt, int cus) {
       p.stream = true;
       p.grid = per_col * n_tiles;
       p.share = (m_tiles * nk + per_col - 1) / per_col;
-      p.slices = 2;
+      p.slices = p.share % nk == 0 ? 1 : 2;
       return p;
     }
     return p;  // split grid, K whole, several rounds
