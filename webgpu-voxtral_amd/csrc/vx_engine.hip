@@ -1485,10 +1485,14 @@ int vx_fill_kv_synthetic(vx_engine *e, uint64_t seed, int32_t npos) {
 // W.normed hold the last token's values and the position is advanced, as
 // after n single steps.
 // The prefill GEMMs (vx_gemm.h): 144 KB of dynamic LDS per block and the
-// device's compute-unit count for the grids.
+// device's compute-unit count for the grids; the prompt attention's 71 KB.
 static int pf_gemm_setup(vx_engine *e) {
   if (e->gemm_ready) return VX_OK;
   HIPCHK(e, gemm_setup());
+  HIPCHK(e, hipFuncSetAttribute((const void *)pf_attn_mfma_kernel<float>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, PFA_LDS));
+  HIPCHK(e, hipFuncSetAttribute((const void *)pf_attn_mfma_kernel<uint16_t>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, PFA_LDS));
   int dev = 0;
   HIPCHK(e, hipGetDevice(&dev));
   HIPCHK(e, hipDeviceGetAttribute(&e->cus, hipDeviceAttributeMultiprocessorCount, dev));
@@ -1549,13 +1553,13 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
                          e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
     });
     if (e->kv_f32 && VX_PF_ATTN_MFMA)
-      hipLaunchKernelGGL(pf_attn_mfma_kernel<float>, dim3(nt / PFA_T, NKV), blk, 0, st, e->pf_q,
-                         (const float *)e->kc(l), (const float *)e->vc(l), e->max_seq, pos0, n, nt,
-                         e->pf_b);
-    else if (VX_PF_ATTN_MFMA)
-      hipLaunchKernelGGL(pf_attn_mfma_kernel<uint16_t>, dim3(nt / PFA_T, NKV), blk, 0, st, e->pf_q,
-                         (const uint16_t *)e->kc(l), (const uint16_t *)e->vc(l), e->max_seq, pos0,
+      hipLaunchKernelGGL(pf_attn_mfma_kernel<float>, dim3(nt / PFA_T, NKV), dim3(256 * PFA_KG), PFA_LDS,
+                         st, e->pf_q, (const float *)e->kc(l), (const float *)e->vc(l), e->max_seq, pos0,
                          n, nt, e->pf_b);
+    else if (VX_PF_ATTN_MFMA)
+      hipLaunchKernelGGL(pf_attn_mfma_kernel<uint16_t>, dim3(nt / PFA_T, NKV), dim3(256 * PFA_KG),
+                         PFA_LDS, st, e->pf_q, (const uint16_t *)e->kc(l), (const uint16_t *)e->vc(l),
+                         e->max_seq, pos0, n, nt, e->pf_b);
     else if (e->kv_f32)
       hipLaunchKernelGGL(pf_attn_kernel<float>, dim3(nt, NKV), blk, 0, st, e->pf_q, e->kc(l),
                          e->vc(l), e->max_seq, pos0, n, nt, e->pf_b);

@@ -280,10 +280,14 @@ __global__ __launch_bounds__(256) void pf_attn_kernel(const float *Q, const void
 
 // ------------------------------------------------ causal attention on MFMA
 // The same result as pf_attn_kernel<float> (attnScore + softmax + attnValue
-// per prompt token over keys 0..pos0+t, src/shaders.ts:306-447) with the
-// products on the matrix cores.  Block = (16-token tile, KV head), wave w =
-// query head 4*kv_head + w; the tile's K and V rows (f32 cache) are staged
-// through LDS 32 keys at a time, V transposed, and shared by the 4 waves.
+// per prompt token over keys 0..pos0+t, src/shaders.ts:306-447) up to the
+// order of the softmax sums, with the products on the matrix cores.
+// Block = (16-token tile, KV head) of PFA_KG groups of 4 waves; wave w of a
+// group is query head 4*kv_head + w.  The tile's keys are taken 32 at a
+// time: group g stages tiles g, g + PFA_KG, ... in its own LDS area, K rows
+// and transposed V rows already split into f16 hi and lo (once per group,
+// not once per wave), shared by its 4 waves, and keeps its own online
+// softmax; the groups' (max, sum, O) are merged through LDS at the end.
 // Per 32-key tile and wave, in the transposed form (the token is the MFMA
 // column, so every lane holds one token's values):
 //   S^T[16 keys][16 tokens] = K[16][128] . Q^T[128][16]     16x16x32 f16
@@ -293,15 +297,24 @@ __global__ __launch_bounds__(256) void pf_attn_kernel(const float *Q, const void
 // softmax rescale of O^T is per lane.  Every f32 operand is split into f16
 // hi + lo and a product is hi.hi + hi.lo + lo.hi, about 2^-20 relative (the
 // dropped lo.lo term), where the prefill GEMMs, with exact f16 weights, are
-// at the split's 2^-21.  Output: hi/lo
+// at the split's 2^-21.  An f16 cache is exact in f16: its lo halves are
+// zero, so they are neither stored nor multiplied.  Output: hi/lo
 // rows of the O projection's B (rows t and nt + t), zero for t >= n.
 typedef _Float16 hf4 __attribute__((ext_vector_type(4)));
-constexpr int PFA_T = 16;        // tokens per block
-constexpr int PFA_K = 32;        // keys per staged tile
-constexpr int PFA_KW = HD + 4;   // LDS row of K (floats)
-constexpr int PFA_VW = PFA_K + 4;  // LDS row of V^T (floats)
+constexpr int PFA_T = 16;          // tokens per block
+constexpr int PFA_K = 32;          // keys per staged tile
+constexpr int PFA_KW = HD + 8;     // LDS row of K, halves (272 B)
+constexpr int PFA_VW = PFA_K + 4;  // LDS row of V^T, halves (72 B: 16 rows start on 16 distinct even banks)
+#ifndef VX_PFA_KG
+#define VX_PFA_KG 2
+#endif
+constexpr int PFA_KG = VX_PFA_KG;  // key groups per block
+constexpr int PFA_GROUP = 2 * (PFA_K * PFA_KW + HD * PFA_VW);  // halves of one group's area (hi + lo)
+constexpr int PFA_LDS = PFA_KG * PFA_GROUP * 2;                // dynamic LDS bytes (70 KB)
+constexpr int PFA_RED = 2 + 4 * (HD / 16);                     // merged values per lane: m, l, O^T
+static_assert((PFA_KG - 1) * 4 * PFA_RED * 64 * 4 <= PFA_LDS, "merge area");
 
-// hi/lo operand halves (split2) of 8 or 4 staged f32 values
+// hi/lo operand halves (split2) of 8 or 4 f32 values
 __device__ __forceinline__ void split8(const f32x4 a, const f32x4 b, h8 &hi, h8 &lo) {
   const float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   split_n<8>(x, hi, lo);
@@ -322,25 +335,31 @@ __device__ __forceinline__ f32x4 pfa_widen(uint2 v) {
   return f32x4{(float)a.x, (float)a.y, (float)b.x, (float)b.y};
 }
 
-// KVT = float (f32 cache) or uint16_t (f16 cache: widened exactly to f32 on
-// staging, so its lo halves are zero and the products are exact)
+// KVT = float (f32 cache) or uint16_t (f16 cache).
+// Launch: grid (nt / PFA_T, NKV), 256 * PFA_KG threads, PFA_LDS dynamic LDS.
 template <typename KVT>
-__global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const KVT *kc, const KVT *vc,
-                                                           int max_seq, int pos0, int n, int nt, h8 *B) {
+__global__ __launch_bounds__(256 * PFA_KG) void pf_attn_mfma_kernel(const float *Q, const KVT *kc,
+                                                                    const KVT *vc, int max_seq, int pos0,
+                                                                    int n, int nt, h8 *B) {
+  constexpr bool EXACT = std::is_same<KVT, uint16_t>::value;  // f16 cache: no lo halves
+  extern __shared__ __attribute__((aligned(16))) _Float16 pfa_smem[];
   const int t0 = blockIdx.x * PFA_T, kvh = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int h = kvh * (NH / NKV) + wave;
+  const int grp_k = wave >> 2, hw = wave & 3;  // key group, head within the KV group
+  const int h = kvh * (NH / NKV) + hw;
   const int col = lane & 15, grp = lane >> 4;  // MFMA column (token) and row group
   const int t = t0 + col;                      // this lane's token
-  __shared__ __attribute__((aligned(16))) float ks[PFA_K * PFA_KW];
-  __shared__ __attribute__((aligned(16))) float vt[HD * PFA_VW];
-  if (t0 >= n) {  // padding columns of the GEMM: zero hi and lo
-    _Float16 *p = (_Float16 *)B;
+  _Float16 *khs = pfa_smem + grp_k * PFA_GROUP, *kls = khs + PFA_K * PFA_KW;
+  _Float16 *vhs = kls + PFA_K * PFA_KW, *vls = vhs + HD * PFA_VW;
+  if (t0 >= n) {  // padding columns of the GEMM: zero hi and lo (group 0 writes)
+    if (grp_k == 0) {
+      _Float16 *p = (_Float16 *)B;
 #pragma unroll
-    for (int dt = 0; dt < HD / 16; dt++) {
-      const size_t c = (size_t)h * HD + dt * 16 + 4 * grp;
-      *(hf4 *)(p + (size_t)t * QD + c) = hf4{0, 0, 0, 0};
-      *(hf4 *)(p + (size_t)(nt + t) * QD + c) = hf4{0, 0, 0, 0};
+      for (int dt = 0; dt < HD / 16; dt++) {
+        const size_t c = (size_t)h * HD + dt * 16 + 4 * grp;
+        *(hf4 *)(p + (size_t)t * QD + c) = hf4{0, 0, 0, 0};
+        *(hf4 *)(p + (size_t)(nt + t) * QD + c) = hf4{0, 0, 0, 0};
+      }
     }
     return;
   }
@@ -349,19 +368,28 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const
   const int last = pos0 + min(t, n - 1);         // last key of this lane's token
   const int kend = pos0 + min(t0 + PFA_T, n);    // keys of the tile: [0, kend)
   const int ntile = (kend + PFA_K - 1) / PFA_K;
+  const int iters = (ntile + PFA_KG - 1) / PFA_KG;  // the same count in every group
 
-  // staging: thread i holds 4 x 4 values of K and of V: row (i / 32) + 8j, dims 4*(i % 32)
-  const int srow = tid >> 5, sdim = (tid & 31) * 4;
+  // staging, thread i of its group: K rows (i / 32) + 8j, dims 4 (i % 32)
+  // (row-major LDS writes); V keys 2 (i % 16) and 2 (i % 16) + 1, dims
+  // 4 (i / 16) and 64 + 4 (i / 16), so each transposed LDS write holds the
+  // pair of keys as one dword
+  const int gtid = tid & 255, srow = gtid >> 5, sdim = (gtid & 31) * 4;
+  const int vkey = 2 * (gtid & 15), vdim = 4 * (gtid >> 4);
   decltype(pfa_ld4(Kb)) kr[4], vr[4];
   auto load_tile = [&](int kb) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int key = min(kb + srow + 8 * j, kend - 1);  // rows past the keys re-read the last
       kr[j] = pfa_ld4(Kb + (size_t)key * HD + sdim);
-      vr[j] = pfa_ld4(Vb + (size_t)key * HD + sdim);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {  // vr[j]: key vkey + (j >> 1), dims vdim + 64 (j & 1)
+      const int key = min(kb + vkey + (j >> 1), kend - 1);
+      vr[j] = pfa_ld4(Vb + (size_t)key * HD + vdim + 64 * (j & 1));
     }
   };
-  load_tile(0);
+  if (grp_k < ntile) load_tile(grp_k * PFA_K);
 
   // Q^T operand of S^T (token t, dims 32c + 8grp..+8), hi and lo; padding tokens zero
   h8 qh[HD / 32], ql[HD / 32];
@@ -380,32 +408,49 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const
 #pragma unroll
   for (int dt = 0; dt < HD / 16; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int it = 0; it < ntile; it++) {
-    const int kb = it * PFA_K;
+  for (int i = 0; i < iters; i++) {
+    const int it = grp_k + PFA_KG * i, kb = it * PFA_K;
+    const bool live = it < ntile;  // uniform over the group
     __syncthreads();  // the previous tile's LDS reads are done
+    if (live) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int r = srow + 8 * j;
-      const f32x4 kw = pfa_widen(kr[j]), vw = pfa_widen(vr[j]);
-      *(f32x4 *)(ks + r * PFA_KW + sdim) = kw;
+      for (int j = 0; j < 4; j++) {
+        hf4 hi, lo;
+        split4(pfa_widen(kr[j]), hi, lo);
+        *(hf4 *)(khs + (srow + 8 * j) * PFA_KW + sdim) = hi;
+        if (!EXACT) *(hf4 *)(kls + (srow + 8 * j) * PFA_KW + sdim) = lo;
+      }
 #pragma unroll
-      for (int q = 0; q < 4; q++) vt[(sdim + q) * PFA_VW + r] = vw[q];
+      for (int hd = 0; hd < 2; hd++) {
+        const f32x4 va = pfa_widen(vr[hd]), vb = pfa_widen(vr[2 + hd]);  // keys vkey, vkey + 1
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          h2 hi, lo;
+          split2(va[q], vb[q], hi, lo);
+          const int d = vdim + 64 * hd + q;
+          *(h2 *)(vhs + d * PFA_VW + vkey) = hi;
+          if (!EXACT) *(h2 *)(vls + d * PFA_VW + vkey) = lo;
+        }
+      }
+      if (it + PFA_KG < ntile) load_tile(kb + PFA_KG * PFA_K);
     }
-    if (it + 1 < ntile) load_tile(kb + PFA_K);
     __syncthreads();
+    if (!live) continue;
 
     // S^T for keys kb + 16kt + (4grp..+3), token col
     f32x4 s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-      const float *kp = ks + (16 * kt + col) * PFA_KW + 8 * grp;
+      const int ro = (16 * kt + col) * PFA_KW + 8 * grp;
 #pragma unroll
       for (int c = 0; c < HD / 32; c++) {
-        h8 kh, kl;
-        split8(*(const f32x4 *)(kp + 32 * c), *(const f32x4 *)(kp + 32 * c + 4), kh, kl);
+        const h8 kh = *(const h8 *)(khs + ro + 32 * c);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[c], acc, 0, 0, 0);
+        if (!EXACT) {
+          const h8 kl = *(const h8 *)(kls + ro + 32 * c);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[c], acc, 0, 0, 0);
+        }
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], acc, 0, 0, 0);
       }
       s[kt] = acc;
@@ -415,23 +460,25 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int key = kb + 16 * kt + 4 * grp + i;
-        const float v = key <= last ? s[kt][i] * scale : -INFINITY;
-        s[kt][i] = v;
+      for (int q = 0; q < 4; q++) {
+        const int key = kb + 16 * kt + 4 * grp + q;
+        const float v = key <= last ? s[kt][q] * scale : -INFINITY;
+        s[kt][q] = v;
         mx = fmaxf(mx, v);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx);  // finite: key 0 <= last is in the first tile
-    const float corr = expf(m - mnew);
+    // a token whose keys all lie past this tile's start keeps m = -inf
+    // (only in groups other than 0: key 0 <= last is in tile 0)
+    const float mnew = fmaxf(m, mx);
+    const float corr = mnew == -INFINITY ? 1.0f : expf(m - mnew);
     float ps = 0.f;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float e = s[kt][i] == -INFINITY ? 0.f : expf(s[kt][i] - mnew);
-        s[kt][i] = e;
+      for (int q = 0; q < 4; q++) {
+        const float e = s[kt][q] == -INFINITY ? 0.f : expf(s[kt][q] - mnew);
+        s[kt][q] = e;
         ps += e;
       }
     ps += __shfl_xor(ps, 16, 64);
@@ -447,13 +494,54 @@ __global__ __launch_bounds__(256) void pf_attn_mfma_kernel(const float *Q, const
       f32x4 acc = o[dt] * corr;
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
-        hf4 vh, vl;
-        split4(*(const f32x4 *)(vt + (16 * dt + col) * PFA_VW + 16 * kt + 4 * grp), vh, vl);
+        const int ro = (16 * dt + col) * PFA_VW + 16 * kt + 4 * grp;
+        const hf4 vh = *(const hf4 *)(vhs + ro);
         acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, ph[kt], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph[kt], acc, 0, 0, 0);
+        if (!EXACT) {
+          const hf4 vl = *(const hf4 *)(vls + ro);
+          acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph[kt], acc, 0, 0, 0);
+        }
         acc = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, pl[kt], acc, 0, 0, 0);
       }
       o[dt] = acc;
+    }
+  }
+  // merge the groups' (m, l, O^T) in group order: groups 1.. write theirs
+  // to LDS (lane-minor), group 0 combines them
+  if (PFA_KG > 1) {
+    float *red = (float *)pfa_smem;
+    __syncthreads();  // every group is done with its staging area
+    if (grp_k > 0) {
+      float *r = red + ((grp_k - 1) * 4 + hw) * PFA_RED * 64 + lane;
+      r[0] = m;
+      r[64] = l;
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; dt++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) r[(2 + 4 * dt + q) * 64] = o[dt][q];
+    }
+    __syncthreads();
+    if (grp_k > 0) return;
+    float mg[PFA_KG];
+    mg[0] = m;
+#pragma unroll
+    for (int g = 1; g < PFA_KG; g++) mg[g] = red[((g - 1) * 4 + hw) * PFA_RED * 64 + lane];
+    float mm = mg[0];
+#pragma unroll
+    for (int g = 1; g < PFA_KG; g++) mm = fmaxf(mm, mg[g]);
+    const float c0 = expf(m - mm);  // m is finite in group 0
+    l *= c0;
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++) o[dt] = o[dt] * c0;
+#pragma unroll
+    for (int g = 1; g < PFA_KG; g++) {
+      const float *rg = red + ((g - 1) * 4 + hw) * PFA_RED * 64 + lane;
+      const float cg = mg[g] == -INFINITY ? 0.f : expf(mg[g] - mm);
+      l += rg[64] * cg;
+#pragma unroll
+      for (int dt = 0; dt < HD / 16; dt++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) o[dt][q] += rg[(2 + 4 * dt + q) * 64] * cg;
     }
   }
   // out[t][dims] = O^T / l, as hi and lo f16 rows of B (zero past n)
