@@ -14,7 +14,9 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
-LIB_PATH = os.path.join(PKG, "lib", "libvoxtral_amd.so")
+# VOXTRAL_AMD_LIB selects another build of the library (e.g. the host-
+# sanitizer build of `make asan`)
+LIB_PATH = os.environ.get("VOXTRAL_AMD_LIB") or os.path.join(PKG, "lib", "libvoxtral_amd.so")
 HEADER = os.path.join(os.path.dirname(PKG), "include", "voxtral_engine.h")
 
 VX_OK, VX_E_INVALID, VX_E_STATE, VX_E_DEVICE, VX_E_RANGE, VX_E_NOMEM = 0, -1, -2, -3, -4, -5
