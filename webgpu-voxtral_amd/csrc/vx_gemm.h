@@ -25,8 +25,8 @@
 //  - gemm_split_kernel: one tile per block, K split in KS = gridDim.y
 //    slices (S_out = KS); for shapes with at most one block per CU.
 //  - gemm_stream_kernel: one block per CU, each doing an equal share of the
-//    column tile's (row tile, k-tile) sequence, at most 2 blocks per tile
-//    (S_out = 2, or 1 when the shares are whole tiles); for shapes with more
+//    column tile's (row tile, k-tile) sequence; S_out = the most blocks a
+//    tile is split over (rounded up to 1, 2, 4 or 8); for shapes with more
 //    tiles than CUs, which would otherwise run in uneven rounds.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -257,16 +257,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
 // Balanced grid: G blocks (G / 8 a multiple of n_tiles).  Block lb works on
 // column tile c = lb % n_tiles, share j = lb / n_tiles of that column's
-// sequence g = mt * nk + kt, g in [j L, (j + 1) L) with L >= nk, so a tile
-// is done by at most two blocks.  The part of a tile that starts at kt = 0
-// goes to C block 0, the other part to block 1; a tile done by one block
-// writes zeros to block 1, unless every share is whole tiles (then only
-// block 0 is written and the consumer reads one slice).  The n_tiles blocks of a share read the same
-// weight k-tiles at the same time; XCD x (blocks b with b % 8 == x) holds
-// whole shares, so one L2 serves them.
+// sequence g = mt * nk + kt, g in [j L, (j + 1) L).  A tile is split into
+// the segments of the blocks whose shares overlap it; the segment of block j
+// goes to C block j - j0(mt), j0(mt) = mt nk / L (its first block), and the
+// block holding a tile's last segment writes zeros to the C blocks after it,
+// up to the ns blocks the consumer reads.  The n_tiles blocks of a share
+// read the same weight k-tiles at the same time; XCD x (blocks b with
+// b % 8 == x) holds whole shares, so one L2 serves them.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stream_kernel(
     const uint16_t *__restrict__ W, int M, int K, const uint16_t *__restrict__ B, int nt, float *__restrict__ C,
-    int ldc, int Lshare) {
+    int ldc, int Lshare, int ns) {
   extern __shared__ __attribute__((aligned(16))) unsigned char gm_smem[];
   const GmLane L(threadIdx.x);
   const int n_tiles = nt / GM_BN, m_tiles = M / GM_BM, nk = K / GM_BK;
@@ -277,8 +277,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int g0 = min(j * Lshare, total), g1 = min(g0 + Lshare, total);
   if (g0 >= g1) return;
   const int last = g1 - 1;
-  // shares of whole tiles: every tile is done by one block, C block 1 unused
-  const bool whole = Lshare % nk == 0;
+  const size_t slot_stride = (size_t)nt * ldc;
   // per-lane offsets of the direct loads from the k-tile's weight / B origin
   size_t off[GM_LOADS];
 #pragma unroll
@@ -293,6 +292,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   gm_f32x16 acc[2][2];
   gm_zero(acc);
+  // zeros for the C blocks past each tile whose last segment is this
+  // block's (issued before the ring's first loads, so the stores are older
+  // than every load the pipeline counts)
+  for (int mt = g0 / nk; mt <= last / nk; mt++) {
+    if ((mt + 1) * nk - 1 > last) break;  // the tile goes on in the next block
+    for (int sl = j - mt * nk / Lshare + 1; sl < ns; sl++)
+      gm_store(L, acc, C + sl * slot_stride, ldc, c * GM_BN, mt * GM_BM, true);
+  }
   gm_h8 f0[6], f1[6];
 #pragma unroll
   for (int s = 0; s < GM_S; s++) {
@@ -329,20 +336,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
   int stage = 0, pend_stage = 0;
   int c_mt = g0 / nk, c_kt = g0 - c_mt * nk;  // tile and k-tile of iteration g
-  int seg_k0 = c_kt;                           // where this block's part of the tile started
   int stored = 0;                              // stores issued at the end of the last iteration
   auto tail = [&]() {
-    const bool end_tile = c_kt == nk - 1;
     stored = 0;
-    if (end_tile || g == last) {
-      gm_store(L, acc, C + (seg_k0 == 0 ? 0 : (size_t)nt * ldc), ldc, c * GM_BN, c_mt * GM_BM, false);
+    if (c_kt == nk - 1 || g == last) {
+      const int slot = j - c_mt * nk / Lshare;  // this segment's C block
+      gm_store(L, acc, C + slot * slot_stride, ldc, c * GM_BN, c_mt * GM_BM, false);
       stored = 16;
-      if (seg_k0 == 0 && end_tile && !whole) {
-        gm_store(L, acc, C + (size_t)nt * ldc, ldc, c * GM_BN, c_mt * GM_BM, true);
-        stored = 32;
-      }
       gm_zero(acc);
-      seg_k0 = 0;
     }
     if (++c_kt == nk) {
       c_kt = 0;
@@ -383,22 +384,37 @@ inline bool gm_with_slices(int ns, F &&f) {
   }
 }
 
+// Consumer slice count of a balanced grid with per_col shares of L k-tiles
+// per column: the most segments any tile is cut into, rounded up to 1, 2, 4
+// or 8 (0: more than 8)
+inline int gemm_stream_slices(int m_tiles, int nk, int L) {
+  int most = 1;
+  for (int mt = 0; mt < m_tiles; mt++) {
+    const int segs = (mt * nk + nk - 1) / L - mt * nk / L + 1;
+    if (segs > most) most = segs;
+  }
+  return most == 1 ? 1 : most == 2 ? 2 : most <= 4 ? 4 : most <= 8 ? 8 : 0;
+}
+
 // cus: the device's compute units (8 XCDs).  Shapes must satisfy
 // M % 256 == 0, nt % 64 == 0, K % 64 == 0.
 inline GemmPlan gemm_plan(int M, int K, int nt, int cus) {
   GemmPlan p;
   const int m_tiles = M / GM_BM, n_tiles = nt / GM_BN, tiles = m_tiles * n_tiles, nk = K / GM_BK;
   if (tiles > cus) {
-    const int per_col = 8 * ((cus / 8) / n_tiles);  // shares per column tile
+    const int per_col = 8 * ((cus / 8) / n_tiles);  // balanced grid: shares per column tile
     if (per_col >= 8 && m_tiles >= per_col) {
       p.stream = true;
       p.grid = per_col * n_tiles;
       p.share = (m_tiles * nk + per_col - 1) / per_col;
-      p.slices = p.share % nk == 0 ? 1 : 2;
+      p.slices = gemm_stream_slices(m_tiles, nk, p.share);
       return p;
     }
     return p;  // split grid, K whole, several rounds
   }
+  // At most one block per CU: K split in KS slices.  (The balanced grid on
+  // all CUs, with a tile cut into up to 8 segments, measured slower for these
+  // shapes: QKV, O and down of the 256-token prompt took 2-5 us more each.)
   while (p.ks < 8 && tiles * p.ks * 2 <= cus && (nk % (p.ks * 2)) == 0 && nk / (p.ks * 2) >= 2) p.ks *= 2;
   p.slices = p.ks;
   return p;
@@ -415,7 +431,8 @@ inline hipError_t gemm_setup() {
 inline void gemm_launch(const GemmPlan &p, hipStream_t st, const uint16_t *W, int M, int K, const uint16_t *B,
                         int nt, float *C) {
   if (p.stream)
-    hipLaunchKernelGGL(gemm_stream_kernel, dim3(p.grid), dim3(256), GM_LDS, st, W, M, K, B, nt, C, M, p.share);
+    hipLaunchKernelGGL(gemm_stream_kernel, dim3(p.grid), dim3(256), GM_LDS, st, W, M, K, B, nt, C, M, p.share,
+                       p.slices);
   else
     hipLaunchKernelGGL(gemm_split_kernel, dim3((M / GM_BM) * (nt / GM_BN), p.ks), dim3(256), GM_LDS, st, W, M, K,
                        B, nt, C, M);
