@@ -128,6 +128,39 @@ def test_prefill_two_chunks_after_context():
         o.close()
 
 
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_prefill_after_long_context(kv_f16):
+    """96 prompt tokens on top of 2000 synthetic cache positions: every
+    16-token query tile of the prompt attention walks 63-66 key tiles, split
+    over its key groups and merged at the end.  The new K/V rows (f32 cache
+    to 1e-3; f16 cache within one f16 ulp of the oracle's own f16 rounding,
+    to 1e-2) and the last W.normed."""
+    print(f"[prefill] 1 layer, 2000 cached + 96 tokens, f16 KV {kv_f16}", flush=True)
+    from vxtest import fill_oracle_kv
+    g = gpu_engine(n_layers=1, max_seq=2304, kv_f16=kv_f16)
+    o = oracle_engine(n_layers=1, max_seq=2304)
+    try:
+        if kv_f16:
+            o.set_kv_f16(True)
+        g.fill_kv_synthetic(SEED, 2000)
+        fill_oracle_kv(o, SEED, 2000)
+        g.position = 2000
+        o.position = 2000
+        tokens = np.random.default_rng(21).integers(0, 131072, 96)
+        g.prefill(tokens)
+        oracle_prefill(o, tokens, 0, 0, None)
+        assert g.position == 2096
+        bar = 1e-2 if kv_f16 else 1e-3
+        for w in (0, 1):
+            got = g.read_kv(0, w, 2000, 96)
+            ref = o.kv(0, w)[2000:2096]
+            assert max_rel_err(got, ref) < bar, (w, max_rel_err(got, ref))
+        assert max_rel_err(g.debug_read("normed", 3072), o.buffer("normed")) < bar
+    finally:
+        g.destroy()
+        o.close()
+
+
 def test_prefill_argument_errors():
     import voxtral_amd as V
     g = gpu_engine(n_layers=1, max_seq=64)
