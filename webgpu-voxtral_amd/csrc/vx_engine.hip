@@ -298,7 +298,7 @@ void launch_gemv1(hipStream_t st, const GemvArgs &a) {
                      dim3(WAVES * 64), 0, st, a);
 }
 // unit counts of the backbone GEMVs must split into whole blocks
-static_assert((QKV_ROWS / 2) % 4 == 0 && DIM % 6 == 0 && HID % 12 == 0 && DIM % 4 == 0,
+static_assert((QKV_ROWS / 2) % 6 == 0 && DIM % 4 == 0 && HID % 12 == 0 && DIM % 6 == 0,
               "launch shapes");
 
 // One backbone layer: 6 launches (norm + QKV + rope + KV write | attention
@@ -317,7 +317,7 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
     a.kv_f32 = e->kv_f32;
     a.max_seq = e->max_seq;
     a.inv_freq = e->inv_freq;
-    launch_gemv1<4, 1, 1, EPI_QKV_ROPE, true, DIM, 1>(st, a);
+    launch_gemv1<6, 1, 1, EPI_QKV_ROPE, true, DIM, 1>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_ATTN) {
     AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn};
@@ -329,7 +329,7 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
     GemvArgs a = gargs(W.wo, e->attn, QD, e->x, 0, DIM);
-    launch_gemv1<6, 1, 1, EPI_RESID, false, QD, 1>(st, a);
+    launch_gemv1<4, 1, 1, EPI_RESID, false, QD, 1>(st, a);
   }
   if (only < 0 || only == VX_KERNEL_GATEUP) {
     GemvArgs a = gargs(W.w1, e->x, DIM, e->act, 0, HID);
@@ -340,7 +340,7 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
   }
   if (only < 0 || only == VX_KERNEL_DOWN) {
     GemvArgs a = gargs(W.w2, e->act, HID, e->x, 0, DIM);
-    launch_gemv1<4, 1, 1, EPI_RESID, false, HID, 1>(st, a);
+    launch_gemv1<6, 1, 1, EPI_RESID, false, HID, 1>(st, a);
   }
 }
 
