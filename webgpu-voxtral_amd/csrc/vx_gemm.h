@@ -209,9 +209,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   extern __shared__ __attribute__((aligned(16))) unsigned char gm_smem[];
   const GmLane L(threadIdx.x);
   const int n_tiles = nt / GM_BN, m_tiles = M / GM_BM;
-  // tiles m-major; XCD x (blocks b with b % 8 == x, dispatched in order)
-  // takes the x-th eighth, so the column tiles sharing a weight tile run
-  // together on one XCD and its L2 serves the re-reads
+  // tiles m-major; the blocks b with b % 8 == x take the x-th eighth.
+  // Workgroups are dealt to the 8 XCDs round-robin (from a starting XCD that
+  // varies between launches), so blocks with equal b % 8 share an XCD: the
+  // column tiles sharing a weight tile run together and one L2 serves the
+  // re-reads
   int mt, ntl;
   {
     const int b = blockIdx.x, tiles = m_tiles * n_tiles;
@@ -262,8 +264,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 // goes to C block j - j0(mt), j0(mt) = mt nk / L (its first block), and the
 // block holding a tile's last segment writes zeros to the C blocks after it,
 // up to the ns blocks the consumer reads.  The n_tiles blocks of a share
-// read the same weight k-tiles at the same time; XCD x (blocks b with
-// b % 8 == x) holds whole shares, so one L2 serves them.
+// read the same weight k-tiles at the same time; the blocks b with equal
+// b % 8 (one XCD, as workgroups are dealt to the XCDs round-robin) hold
+// whole shares, so one L2 serves them.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stream_kernel(
     const uint16_t *__restrict__ W, int M, int K, const uint16_t *__restrict__ B, int nt, float *__restrict__ C,
     int ldc, int Lshare, int ns) {
