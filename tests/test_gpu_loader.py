@@ -88,6 +88,13 @@ def test_loader_errors(tmp_path):
         bad.write_bytes(struct.pack("<Q", 5) + b"{oops")
         with pytest.raises(V.VoxtralError, match="header"):
             g.load_safetensors(bad)
+        # a deeply nested value (rejected, not recursed into) and an offset
+        # outside int64
+        for hdr in (b'{"__metadata__":' + b"[" * 200000 + b"]" * 200000 + b"}",
+                    b'{"norm.weight":{"dtype":"F16","shape":[3072],"data_offsets":[0,99999999999999999999]}}'):
+            bad.write_bytes(struct.pack("<Q", len(hdr)) + hdr)
+            with pytest.raises(V.VoxtralError, match="header"):
+                g.load_safetensors(bad)
         p = tmp_path / "dtype.safetensors"
         write_safetensors(p, {"layers.0.ffn_norm.weight": ("I32", np.zeros(3072, np.int32))})
         with pytest.raises(V.VoxtralError, match="Unsupported dtype for layers.0.ffn_norm.weight: I32"):

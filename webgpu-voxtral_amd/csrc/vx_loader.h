@@ -143,8 +143,9 @@ class StHeaderParser {
     }
     uint64_t x = 0;
     while (p_ < end_ && *p_ >= '0' && *p_ <= '9') {
-      if (x > (UINT64_MAX - 9) / 10) return false;
-      x = x * 10 + (uint64_t)(*p_++ - '0');
+      const uint64_t d = (uint64_t)(*p_++ - '0');
+      if (x > ((uint64_t)INT64_MAX - d) / 10) return false;  // outside int64
+      x = x * 10 + d;
     }
     v = neg ? -(int64_t)x : (int64_t)x;
     return true;
@@ -194,9 +195,12 @@ class StHeaderParser {
       return false;
     }
   }
-  bool skip_value() {
+  // nesting deeper than kMaxDepth is rejected (a header of nested brackets
+  // must not exhaust the stack)
+  static constexpr int kMaxDepth = 64;
+  bool skip_value(int depth = 0) {
     ws();
-    if (p_ >= end_) return false;
+    if (p_ >= end_ || depth > kMaxDepth) return false;
     if (*p_ == '"') {
       std::string s;
       return str(s);
@@ -214,7 +218,7 @@ class StHeaderParser {
           ws();
           if (!eat(':')) return false;
         }
-        if (!skip_value()) return false;
+        if (!skip_value(depth + 1)) return false;
         ws();
         if (eat(',')) continue;
         return eat(close);
