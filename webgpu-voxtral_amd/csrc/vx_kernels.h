@@ -1255,7 +1255,7 @@ __global__ __launch_bounds__(TP_NT) void topp_sample_kernel(const float *logits,
   __shared__ uint32_t bcnt[TP_BINS];
   __shared__ uint64_t wsum[TP_WAVES];
   __shared__ double red[TP_WAVES];
-  __shared__ uint64_t sel_base, sel_incl, target;
+  __shared__ uint64_t sel_base, sel_incl, sel_key, target;
   __shared__ int sel;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float *sv = reinterpret_cast<float *>(key);
@@ -1365,6 +1365,16 @@ __global__ __launch_bounds__(TP_NT) void topp_sample_kernel(const float *logits,
       base = sel_base;
       prefix = (prefix << width) | (uint64_t)ds;
       incl = sel_incl;
+      if (bcnt[ds] == 1) {
+        // one key carries this prefix: the later passes would select its
+        // digits with the same inclusive mass, so it is the answer
+        for (int i = tid; i < n; i += TP_NT)
+          if ((key[i] >> shift) == prefix) sel_key = key[i];
+        __syncthreads();
+        kout = sel_key;
+        __syncthreads();  // every thread has read sel_key
+        return true;
+      }
       __syncthreads();  // bins and sel are reset by the next pass
     }
     kout = prefix;
