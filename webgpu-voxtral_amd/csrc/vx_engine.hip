@@ -95,7 +95,7 @@ struct vx_engine {
   void *aarena = nullptr;
   float *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *normed = nullptr,
         *logits = nullptr, *part = nullptr, *layer_stage = nullptr;
-  int *counter = nullptr, *pos = nullptr, *frame = nullptr;
+  int *pos = nullptr, *frame = nullptr;
   uint32_t *sem_code = nullptr, *codes = nullptr, *argmax_res = nullptr;
   uint64_t *noise_seed = nullptr;
   float *inv_freq = nullptr;  // rope inverse frequencies [HD/2]
@@ -991,7 +991,6 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   aplace((void **)&e->logits, (size_t)cfg.vocab_size * 4);
   aplace((void **)&e->part, (size_t)NH * ATTN_SPLITS * (HD + 2) * 4);
   aplace((void **)&e->layer_stage, (size_t)nl * 2 * DIM * 4);
-  aplace((void **)&e->counter, 64 * 4);
   aplace((void **)&e->pos, 4);
   aplace((void **)&e->frame, 4);
   aplace((void **)&e->sem_code, 4);
