@@ -236,9 +236,9 @@ GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, in
 #endif
 
 // FM GEMM launch: `rows` output rows in tiles of FTR, RG tiles per block.
-template <int EPI, int K, int RG, int KS, int P>
+template <int EPI, int K, int RG, int KS, int P, bool KEEP = false>
 void launch_gemm6(hipStream_t st, const Gemm6Args &a, int rows) {
-  hipLaunchKernelGGL((gemm6_kernel<EPI, K, RG, KS, P>), dim3(rows / (FTR * RG)), dim3(RG * KS * 64),
+  hipLaunchKernelGGL((gemm6_kernel<EPI, K, RG, KS, P, KEEP>), dim3(rows / (FTR * RG)), dim3(RG * KS * 64),
                      0, st, a);
 }
 // Launch shapes of the four FM GEMMs <RG, KS, P>, picked on the whole frame
@@ -439,7 +439,14 @@ static void enqueue_fm_kernel(vx_engine *e, int l, int k, int nssq_attn) {
       a.Bn = e->fm_b_ffn;
       a.gn = W.ffn_norm;
       a.ssq_out = e->fm_ssq_ffn;
-      FM_GEMM_O(st, a, DIM);
+      // Layer 0's O matrix (25 MB, about 3.1 MB per XCD's 4 MB L2) is read
+      // with plain loads, so much of it is still in L2 at the next Euler
+      // step (6.3 against 7.5 us per launch); every other weight stream is
+      // non-temporal.  Only one FM matrix fits.
+      if (l == 0)
+        launch_gemm6<EPI_RESID, QD, 1, 16, 4, true>(st, a, DIM);
+      else
+        FM_GEMM_O(st, a, DIM);
       break;
     }
     case FMK_GATEUP: {  // RMSNorm + gate/up + SwiGLU; hands the activation to down

@@ -1015,8 +1015,9 @@ struct Gemm6Args {
 
 // Block = RG row tiles x KS k-slices (one wave each); a wave streams its
 // tile's chunks (EPI_SWIGLU: the gate and up tiles), P chunks in flight, and
-// k-slices are summed through LDS.  Grid = rows / (FTR RG).
-template <int EPI, int K, int RG, int KS, int P>
+// k-slices are summed through LDS.  Grid = rows / (FTR RG).  KEEP: plain
+// weight loads (cached in L2) instead of non-temporal ones.
+template <int EPI, int K, int RG, int KS, int P, bool KEEP = false>
 __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
   constexpr int TL = EPI == EPI_SWIGLU ? 2 : 1;
   constexpr int NC = K / 32, NCW = NC / KS;
@@ -1079,7 +1080,8 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
     bb[d] = bp[c * 4 * BCOL];
 #pragma unroll
     for (int t = 0; t < TL; t++)
-      wb[d][t] = ldw(wp[t] + (size_t)c * (4 * FTR * 8));
+      wb[d][t] = KEEP ? *(const u32x4 *)(wp[t] + (size_t)c * (4 * FTR * 8))
+                      : ldw(wp[t] + (size_t)c * (4 * FTR * 8));
   };
 #pragma unroll
   for (int d = 0; d < P; d++) load(d, d);
