@@ -486,18 +486,25 @@ static void enqueue_fm_kernel(vx_engine *e, int l, int k, int nssq_attn) {
 }
 
 // Start of Euler step s (x_s, the input projection, both CFG sequences).
-static void enqueue_fm_step_in(vx_engine *e, int s, const float *noise_src) {
+// The input kernel of Euler step s.  noise_src: x_0 (step 0), or null for
+// the device generator (seed, kNoiseStream, frame counter).  sem_mask >= 0:
+// step 0 also takes the argmax of the semantic logits into sem_code, with
+// argmax_kernel's mask (8194: the greedy code's valid range; 0: unmasked).
+static void enqueue_fm_step_in(vx_engine *e, int s, const float *noise_src, int sem_mask = -1) {
   const float alpha = e->cfg.cfg_alpha;
   const float dt = (float)(1.0 / (double)(e->cfg.nfe - 1));
   FmStepArgs fa{e->xh,      e->vel,    e->ac_part, e->ac_ssq, e->fm_in,
                 e->tproj + (size_t)s * DIM, e->fm_llm_out, e->fm_seq, s, alpha, dt, noise_src,
-                e->fm_b_attn, e->FL[0].attn_norm, e->fm_ssq_attn};
-  hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256), dim3(256), 0, e->st, fa);
+                e->noise_seed, kNoiseStream, e->frame,
+                e->fm_b_attn, e->FL[0].attn_norm, e->fm_ssq_attn,
+                e->sem_logits, sem_mask, e->sem_code};
+  const bool argmax = s == 0 && sem_mask >= 0;
+  hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256 + (argmax ? 1 : 0)), dim3(256), 0, e->st, fa);
 }
 
 // fmForward with CFG batched: 6 vectors (2 branches x 3 positions) share
 // every weight read; time projections come from the precomputed table.
-// noise_src: device f32[36] holding x_0.
+// noise_src: device f32[36] holding x_0, or null for the device generator.
 static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
   hipStream_t st = e->st;
   const float alpha = e->cfg.cfg_alpha;
@@ -507,12 +514,11 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
     launch_gemv<1, W4, 2, EPI_PLAIN, false, DIM, DIM>(st, a);
     GemvArgs b = gargs(e->fm_llm, e->normed, DIM, e->fm_llm_out, 0, DIM);
     launch_gemv<1, W4, 2, EPI_PLAIN, false, DIM, DIM>(st, b);
-    // unmasked tree argmax (W.semantic_argmax), or masked for greedy codes
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, st, e->sem_logits, SEMV,
-                       greedy_code ? 8194 : 0, e->sem_code);
   }
   for (int s = 0; s < e->nsteps(); s++) {
-    enqueue_fm_step_in(e, s, noise_src);
+    // step 0 also takes the unmasked tree argmax (W.semantic_argmax), or the
+    // masked one for greedy codes
+    enqueue_fm_step_in(e, s, noise_src, s == 0 ? (greedy_code ? 8194 : 0) : -1);
     for (int l = 0; l < e->cfg.fm_layers; l++)
       for (int k = FMK_QKV; k <= FMK_DOWN; k++) enqueue_fm_kernel(e, l, k, l == 0 ? DIM / 256 : DIM / FTR);
     // the step's velocities (final norm of position 0 of each branch ->
@@ -538,16 +544,9 @@ static int capture(vx_engine *e, hipGraphExec_t *out, void (*body)(vx_engine *))
 
 // FM part of a frame: seeded device noise, then fmForward; greedy stores
 // the masked argmax as the device semantic code (no host round trip).
-static void fm_greedy_body(vx_engine *e) {
-  hipLaunchKernelGGL(fm_noise_kernel, dim3(1), dim3(64), 0, e->st, e->noise, e->noise_seed,
-                     kNoiseStream, e->frame);
-  enqueue_fm(e, e->noise, true);
-}
-static void fm_plain_body(vx_engine *e) {
-  hipLaunchKernelGGL(fm_noise_kernel, dim3(1), dim3(64), 0, e->st, e->noise, e->noise_seed,
-                     kNoiseStream, e->frame);
-  enqueue_fm(e, e->noise, false);
-}
+// x_0 from the device generator, drawn by the first Euler step's kernel
+static void fm_greedy_body(vx_engine *e) { enqueue_fm(e, nullptr, true); }
+static void fm_plain_body(vx_engine *e) { enqueue_fm(e, nullptr, false); }
 // FM, then the semantic code by device top-p (masked, src/engine.ts:2556-2567)
 static void fm_topp_body(vx_engine *e) {
   fm_plain_body(e);
@@ -1303,13 +1302,8 @@ int vx_fm_forward(vx_engine *e, const float *noise, float *sem_logits, uint32_t 
   int rc = check_ready(e);
   if (rc) return rc;
   if ((rc = ensure_tproj(e))) return rc;
-  if (noise) {
-    HIPCHK(e, hipMemcpyAsync(e->noise, noise, NAC * 4, hipMemcpyHostToDevice, e->st));
-  } else {
-    hipLaunchKernelGGL(fm_noise_kernel, dim3(1), dim3(64), 0, e->st, e->noise, e->noise_seed,
-                       kNoiseStream, e->frame);
-  }
-  enqueue_fm(e, e->noise, false);
+  if (noise) HIPCHK(e, hipMemcpyAsync(e->noise, noise, NAC * 4, hipMemcpyHostToDevice, e->st));
+  enqueue_fm(e, noise ? e->noise : nullptr, false);
   LAUNCHCHK(e);
   if (sem_logits)
     HIPCHK(e, hipMemcpyAsync(sem_logits, e->sem_logits, SEMV * 4, hipMemcpyDeviceToHost, e->st));

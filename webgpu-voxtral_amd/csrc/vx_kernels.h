@@ -770,8 +770,8 @@ __global__ __launch_bounds__(1024) void final_norm_kernel(const float *x, const 
 // argmax with the reference's 256-lane strided scan and tree (strict '>').
 // mask_valid > 0: indices 0 and >= mask_valid count as -inf (the host-side
 // semantic masking of src/engine.ts:2556-2563).
-__global__ __launch_bounds__(256) void argmax_kernel(const float *x, int n, int mask_valid,
-                                                     uint32_t *result) {
+// One block of 256 threads.
+__device__ __forceinline__ void argmax_block(const float *x, int n, int mask_valid, uint32_t *result) {
   __shared__ float bv[256];
   __shared__ uint32_t bi[256];
   const int t = threadIdx.x;
@@ -814,6 +814,10 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *x, int n, int 
     __syncthreads();
   }
   if (t == 0) result[0] = bi[0];
+}
+__global__ __launch_bounds__(256) void argmax_kernel(const float *x, int n, int mask_valid,
+                                                     uint32_t *result) {
+  argmax_block(x, n, mask_valid, result);
 }
 
 // ------------------------------------------------------------- generator
@@ -1448,10 +1452,18 @@ struct FmStepArgs {
   float *seq;            // [2][3][DIM]
   int step;
   float alpha, dt;
-  const float *noise;    // step 0: x_t = noise
+  const float *noise;    // step 0: x_t = noise, or (null) the device generator's
+  const uint64_t *noise_seed;  //   fm_gauss(seed, noise_stream, frame * NAC + i)
+  uint64_t noise_stream;
+  const int *frame;
   h8 *Bn;                // packed input of the first layer's QKV GEMM,
   const uint16_t *gn;    //   times its attention-norm gains,
   float *ssq_out;        //   and sums of squares, vector-major [FMV][SSQ_MAX]
+  // step 0: a block past the grid's DIM / 256 takes the (masked) argmax of
+  // the semantic logits (argmax_kernel's work, off the FM's critical path)
+  const float *sem_logits;
+  int sem_mask;
+  uint32_t *sem_code;
 };
 
 // The velocities of an Euler step (acoustic_codebook_output(RMSNorm(position
@@ -1491,6 +1503,10 @@ __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
   __shared__ float xs[NAC];
   __shared__ float vs[2 * NAC];
   const int t = threadIdx.x;
+  if (blockIdx.x == DIM / 256) {  // launched with this block at step 0 only
+    argmax_block(a.sem_logits, SEMV, a.sem_mask, a.sem_code);
+    return;
+  }
   const int row = blockIdx.x * 256 + t;  // grid covers DIM exactly
   // this row's input-projection weights, time/llm projections and gain do
   // not depend on x_s: issued first, they arrive while x_s is formed
@@ -1506,7 +1522,7 @@ __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
   if (t < NAC) {
     float x;
     if (a.step == 0) {
-      x = a.noise[t];
+      x = a.noise ? a.noise[t] : fm_gauss(*a.noise_seed, a.noise_stream, (uint64_t)(*a.frame) * NAC + t);
     } else {
       x = cfg_euler(a.xh[(a.step - 1) * NAC + t], vs[t], vs[NAC + t], a.alpha, a.dt);
     }
@@ -1594,11 +1610,5 @@ __global__ __launch_bounds__(256) void fm_finish_kernel(float *xh, float *vel, c
   if (t == 0 && frame_counter) *frame_counter += 1;
 }
 
-// Device noise: x_0[i] = fm_gauss(seed, stream, frame*36 + i)
-__global__ void fm_noise_kernel(float *noise, const uint64_t *seed, uint64_t stream,
-                                const int *frame_counter) {
-  const int t = threadIdx.x;
-  if (t < NAC) noise[t] = fm_gauss(*seed, stream, (uint64_t)(*frame_counter) * NAC + t);
-}
 
 }  // namespace vx
