@@ -152,6 +152,15 @@ int vx_prefill(vx_engine *e, const int32_t *tokens, int32_t n_tokens,
 int vx_backbone_step_layers(vx_engine *e, int32_t token, int32_t embed_mode,
                             const float *precomputed, float *layer_out);
 
+/* debugBackboneLayerByLayer, src/engine.ts:2106-2287, with all of its read
+ * points: one step that copies the embedding (the first layer's input) into
+ * embed[dim] and, per layer, the attention RMSNorm output, the hidden state
+ * after the attention residual, the FFN RMSNorm output and the hidden state
+ * after the FFN residual into layers[n_layers][4][dim] (either pointer may
+ * be NULL, not both).  The final norm is W.normed afterwards (vx_read). */
+int vx_debug_backbone_layers(vx_engine *e, int32_t token, int32_t embed_mode,
+                             const float *precomputed, float *embed, float *layers);
+
 /* fmForward (src/engine.ts:1240-1380; public form debugFMStep :2363-2380).
  * noise: f32[36] (debugNoise) or NULL for the engine's seeded generator.
  * Outputs (each nullable): semantic logits f32[8320], acoustic codes

@@ -94,6 +94,7 @@ def lib():
             "vxo_argmax_result": (ctypes.c_uint32, [c_vp]),
             "vxo_backbone_step": (None, [c_vp, c_int, c_int, c_vp, c_int]),
             "vxo_backbone_step_ex": (None, [c_vp, c_int, c_int, c_vp, c_int, c_vp]),
+            "vxo_backbone_step_debug": (None, [c_vp, c_int, c_int, c_vp, c_vp, c_vp]),
             "vxo_backbone_step_codes": (None, [c_vp]),
             "vxo_fm_forward": (None, [c_vp, F32]),
             "vxo_fm_forward_batched": (None, [c_vp, F32]),
@@ -356,6 +357,24 @@ class OracleEngine:
                                    int(bool(lm_head)),
                                    lo.ctypes.data if lo is not None else None)
         return lo
+
+    def backbone_layer_by_layer(self, token=0, mode=0, precomputed=None):
+        """debugBackboneLayerByLayer read points (src/engine.ts:2106-2287):
+        embed and, per layer, attn_norm, attn_out, ffn_norm, ffn_out."""
+        pre = None
+        if precomputed is not None:
+            pre = np.ascontiguousarray(precomputed, np.float32)
+            mode = 2
+        d = self.cfg.dim
+        emb = np.empty(d, np.float32)
+        lay = np.empty((self.cfg.n_layers, 4, d), np.float32)
+        lib().vxo_backbone_step_debug(self._h, int(token), int(mode),
+                                      pre.ctypes.data if pre is not None else None,
+                                      emb.ctypes.data, lay.ctypes.data)
+        names = ("attn_norm", "attn_out", "ffn_norm", "ffn_out")
+        return {"embed": emb,
+                "layers": [{n: lay[i, k] for k, n in enumerate(names)} for i in range(self.cfg.n_layers)],
+                "final_norm": self.buffer("normed").copy(), "hidden": lay[-1, 3].copy()}
 
     def backbone_step_codes(self):
         lib().vxo_backbone_step_codes(self._h)

@@ -871,9 +871,15 @@ float *vxo_buffer(vxo_engine *e, const char *name, int *count) {
 
 /* backboneStep, src/engine.ts:814-1042.  Caller-visible position++ as in
  * every public caller of backboneStep (e.g. src/engine.ts:2341, 2470). */
-void vxo_backbone_step_ex(vxo_engine *e, int token, int mode,
-                          const float *precomputed, int lm_head,
-                          float *layer_out) {
+/* One step; layer_out [n_layers][2][dim] receives the hidden state after
+ * each attention and FFN residual, dbg_embed [dim] the embedding (the first
+ * layer's input) and dbg_layers [n_layers][4][dim] the reference's full
+ * read points attn_norm, attn_out, ffn_norm, ffn_out (each pointer may be
+ * NULL). */
+static void backbone_step_impl(vxo_engine *e, int token, int mode,
+                               const float *precomputed, int lm_head,
+                               float *layer_out, float *dbg_embed,
+                               float *dbg_layers) {
   const vxo_config *c = &e->c;
   const int d = c->dim, qd = c->n_heads * c->head_dim,
             kvd = c->n_kv_heads * c->head_dim, hd = c->hidden_dim;
@@ -886,10 +892,13 @@ void vxo_backbone_step_ex(vxo_engine *e, int token, int mode,
   vxo_embedding(mode == 1 ? e->audio_emb : e->tok_emb, mode == 2 ? 0 : token, d,
                 e->hidden);
   if (mode == 2) memcpy(e->hidden, precomputed, (size_t)d * sizeof(float));
+  if (dbg_embed) memcpy(dbg_embed, e->hidden, (size_t)d * sizeof(float));
   for (int l = 0; l < c->n_layers; l++) {
     const layer_w *L = &e->L[l];
+    float *dl = dbg_layers ? dbg_layers + (size_t)(4 * l) * d : NULL;
     memcpy(e->residual, e->hidden, (size_t)d * sizeof(float));
     vxo_rmsnorm(e->hidden, L->attn_norm, e->normed, d, c->norm_eps);
+    if (dl) memcpy(dl, e->normed, (size_t)d * 4);
     vxo_matvec_f16(L->wq, e->normed, e->q, qd, d);
     vxo_matvec_f16(L->wk, e->normed, e->k, kvd, d);
     vxo_matvec_f16(L->wv, e->normed, e->v, kvd, d);
@@ -913,14 +922,17 @@ void vxo_backbone_step_ex(vxo_engine *e, int token, int mode,
     vxo_matvec_f16(L->wo, e->attn_out, e->hidden, d, qd);
     for (int i = 0; i < d; i++) e->hidden[i] = e->hidden[i] + e->residual[i];
     if (layer_out) memcpy(layer_out + (size_t)(2 * l) * d, e->hidden, (size_t)d * 4);
+    if (dl) memcpy(dl + d, e->hidden, (size_t)d * 4);
     memcpy(e->residual, e->hidden, (size_t)d * sizeof(float));
     vxo_rmsnorm(e->hidden, L->ffn_norm, e->normed, d, c->norm_eps);
+    if (dl) memcpy(dl + 2 * d, e->normed, (size_t)d * 4);
     vxo_matvec_f16(L->w1, e->normed, e->gate, hd, d);
     vxo_matvec_f16(L->w3, e->normed, e->up, hd, d);
     vxo_swiglu(e->gate, e->up, hd);
     vxo_matvec_f16(L->w2, e->gate, e->hidden, d, hd);
     for (int i = 0; i < d; i++) e->hidden[i] = e->hidden[i] + e->residual[i];
     if (layer_out) memcpy(layer_out + (size_t)(2 * l + 1) * d, e->hidden, (size_t)d * 4);
+    if (dl) memcpy(dl + 3 * d, e->hidden, (size_t)d * 4);
   }
   vxo_rmsnorm(e->hidden, e->final_norm, e->normed, d, c->norm_eps);
   if (lm_head) {
@@ -928,6 +940,19 @@ void vxo_backbone_step_ex(vxo_engine *e, int token, int mode,
     e->argmax_result = vxo_argmax(e->logits, c->vocab_size);
   }
   e->position++;
+}
+
+void vxo_backbone_step_ex(vxo_engine *e, int token, int mode,
+                          const float *precomputed, int lm_head,
+                          float *layer_out) {
+  backbone_step_impl(e, token, mode, precomputed, lm_head, layer_out, NULL, NULL);
+}
+
+/* debugBackboneLayerByLayer, src/engine.ts:2106-2287 */
+void vxo_backbone_step_debug(vxo_engine *e, int token, int mode,
+                             const float *precomputed, float *embed,
+                             float *layers) {
+  backbone_step_impl(e, token, mode, precomputed, 0, NULL, embed, layers);
 }
 
 void vxo_backbone_step(vxo_engine *e, int token, int mode,

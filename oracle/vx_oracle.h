@@ -129,6 +129,14 @@ void vxo_backbone_step(vxo_engine *e, int token, int mode,
 void vxo_backbone_step_ex(vxo_engine *e, int token, int mode,
                           const float *precomputed, int lm_head,
                           float *layer_out);
+/* Same step with the read points of debugBackboneLayerByLayer
+ * (src/engine.ts:2106-2287): embed [dim] (the embedding lookup, or the
+ * precomputed row) and layers [n_layers][4][dim] = attn_norm, attn_out
+ * (after the attention residual), ffn_norm, ffn_out (after the FFN
+ * residual); either may be NULL.  No LM head. */
+void vxo_backbone_step_debug(vxo_engine *e, int token, int mode,
+                             const float *precomputed, float *embed,
+                             float *layers);
 /* multiCodebookEmbed of the engine's semantic + acoustic codes into hidden
  * (src/engine.ts:2499-2531), then a backbone step on it. */
 void vxo_backbone_step_codes(vxo_engine *e);

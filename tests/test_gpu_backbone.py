@@ -119,7 +119,7 @@ def test_single_layer_decode_at_128(pair1):
     g.position = 128
     o.position = 128
     res = g.debug_backbone_layer_by_layer(0, precomputed=x)
-    lo = o.backbone_step(precomputed=x, layer_out=True)
+    oref = o.backbone_layer_by_layer(precomputed=x)
     assert g.position == 129 and o.position == 129
     # per-kernel intermediates
     q_err = max_rel_err(g.debug_read("q", 4096), o.buffer("q"))
@@ -135,12 +135,15 @@ def test_single_layer_decode_at_128(pair1):
         new = g.read_kv(0, w, 128, 1)[0]
         ref = o.kv(0, w)[128]
         np.testing.assert_allclose(new, ref, rtol=1e-3, atol=1e-4 * np.abs(ref).max())
-    # hidden states at the reference read points
-    for k, name in ((0, "attn_out"), (1, "ffn_out")):
-        err = max_rel_err(res["layers"][0][name], lo[0, k])
+    # every read point of debugBackboneLayerByLayer (the embedding row is
+    # the precomputed input, copied)
+    assert np.array_equal(res["embed"], oref["embed"])
+    for name in ("attn_norm", "attn_out", "ffn_norm", "ffn_out"):
+        err = max_rel_err(res["layers"][0][name], oref["layers"][0][name])
         print(f"{name} max rel err {err:.2e}")
         assert err < 2e-3
-        assert ref_allclose(res["layers"][0][name], lo[0, k])
+        assert ref_allclose(res["layers"][0][name], oref["layers"][0][name])
+    assert np.array_equal(res["hidden"], res["layers"][0]["ffn_out"])
     err = max_rel_err(res["final_norm"], o.buffer("normed"))
     assert err < 2e-3 and ref_allclose(res["final_norm"], o.buffer("normed"))
 
@@ -173,6 +176,22 @@ def test_step_matches_per_layer_path(pair1):
     g.position = 300
     _, step = g.backbone_step(precomputed=x)
     assert max_rel_err(step, eager) < 1e-6
+
+
+def test_layer_read_points_agree_between_entry_points(pair1):
+    """vx_backbone_step_layers (the two residual read points) and
+    vx_debug_backbone_layers run the same kernels on the same state, so
+    their shared read points are identical."""
+    g, _ = pair1
+    x = O.gen_f32(SEED + 2, "input.hidden", 3072)
+    g.fill_kv_synthetic(SEED, 77)
+    g.position = 77
+    full = g.debug_backbone_layer_by_layer(0, precomputed=x)
+    g.position = 77
+    two = g.backbone_step_layers(0, precomputed=x)
+    assert g.position == 78
+    assert np.array_equal(two[0, 0], full["layers"][0]["attn_out"])
+    assert np.array_equal(two[0, 1], full["layers"][0]["ffn_out"])
 
 
 def test_eager_path_matches_graph(pair1, monkeypatch):

@@ -40,7 +40,7 @@ e.init().then(() => console.log(JSON.stringify({{names, ready, msg, init: 'ok'}}
     assert r["names"] == sorted(["create", "destroy", "loadTensor", "loadSafetensors", "codecDecode",
                                  "tokenizerCreate", "tokenizerEncode",
                                  "initSynthetic", "isReady",
-                                 "reset", "position", "backboneStep", "fmForward",
+                                 "reset", "position", "backboneStep", "backboneLayers", "fmForward",
                                  "setSemanticCode", "read", "generate"])
     assert r["ready"] is False
     assert r["msg"].startswith("Engine not initialized")
@@ -71,11 +71,18 @@ const m = require({json.dumps(JS)});
   const dec = await e.codecDecode(r.semanticCodes, [].concat(...r.acousticCodes));
   const redecoded = dec.length === r.audio.length && dec.every((v, i) => v === r.audio[i]);
   const normed = await e.debugBackboneStepFull(24);
+  const lbl = await e.debugBackboneLayerByLayer(24);
+  const pick = (a) => Array.from(a.slice(0, 8));
+  const layerHeads = lbl.layers.map((L) => [pick(L.attn_norm), pick(L.attn_out), pick(L.ffn_norm),
+                                            pick(L.ffn_out)]);
+  const hiddenIsLast = lbl.hidden.every((v, i) => v === lbl.layers[1].ffn_out[i]);
   e.destroy();
   console.log(JSON.stringify({{sem: r.semanticCodes, ac: r.acousticCodes, n: r.stats.framesGenerated,
                                redecoded,
                                frames, stages, late, audio: r.audio.length,
-                               audio_head: Array.from(r.audio.slice(0, 64)), normed0: normed[0]}}));
+                               audio_head: Array.from(r.audio.slice(0, 64)), normed0: normed[0],
+                               lbl_embed: pick(lbl.embed), lbl_layers: layerHeads,
+                               lbl_final: pick(lbl.final_norm), lbl_hidden_last: hiddenIsLast}}));
 }})().catch((err) => {{ console.error(err); process.exit(3); }});
 """
     print("[napi] node generate, 2 layers, 5 frames", flush=True)
@@ -88,6 +95,8 @@ const m = require({json.dumps(JS)});
         g.init_synthetic(0, 0.02)
         vo = (((np.arange(2 * 3072) * voice) % 13 - 6) * 0.0625).astype(np.float32)  # exact in both
         py = g.generate(tokens, 2, 2, vo, 5, sampling="greedy", seed=3, ignore_eos=True)
+        normed = g.debug_backbone_step_full(24)
+        lbl = g.debug_backbone_layer_by_layer(24)
     finally:
         g.destroy()
     assert r["n"] == 5 and r["sem"] == py["semanticCodes"] and r["ac"] == py["acousticCodes"]
@@ -103,6 +112,17 @@ const m = require({json.dumps(JS)});
     # one decode bit-identical audio.
     head = np.float32(r["audio_head"])
     assert np.array_equal(head, py["audio"][:64])
+    # debugBackboneStepFull and debugBackboneLayerByLayer through Node: the
+    # same kernels on the same state as through Python, bit for bit
+    assert np.float32(r["normed0"]) == normed[0]
+    assert np.array_equal(np.float32(r["lbl_embed"]), lbl["embed"][:8])
+    names = ("attn_norm", "attn_out", "ffn_norm", "ffn_out")
+    assert len(r["lbl_layers"]) == 2
+    for l, got in enumerate(r["lbl_layers"]):
+        for k, name in enumerate(names):
+            assert np.array_equal(np.float32(got[k]), lbl["layers"][l][name][:8]), (l, name)
+    assert np.array_equal(np.float32(r["lbl_final"]), lbl["final_norm"][:8])
+    assert r["lbl_hidden_last"]
 
 
 @pytest.mark.gpu

@@ -61,6 +61,49 @@ def test_backbone_steps_match_float64_model(small):
     assert e.position == len(steps)
 
 
+def test_layer_by_layer_read_points(small):
+    """debugBackboneLayerByLayer's read points: the embedding, each layer's
+    two RMSNorm outputs (attention and FFN inputs, with their gains) and
+    the hidden state after each residual, against the float64 model; the
+    step itself leaves the same state as a plain step."""
+    e = small
+    c = e.cfg
+    cfgd = dict(head_dim=c.head_dim, n_heads=c.n_heads, n_kv_heads=c.n_kv_heads, eps=1e-5, theta=1e6)
+    Ws = [layer_weights(e, f"layers.{i}") for i in range(c.n_layers)]
+    tok = R.f16(e.weight("mm_audio_embeddings.tok_embeddings.weight")).reshape(c.vocab_size, c.dim)
+    kvd = c.n_kv_heads * c.head_dim
+    e.reset()
+    e.backbone_step(41)
+    e.backbone_step(7)
+    plain = e.backbone_step(300, layer_out=True)
+    normed_plain = e.buffer("normed").copy()
+    e.reset()
+    e.backbone_step(41)
+    e.backbone_step(7)
+    res = e.backbone_layer_by_layer(300)
+    assert e.position == 3
+    assert np.array_equal(res["final_norm"], normed_plain)
+    assert np.array_equal(res["hidden"], plain[-1, 1])
+    assert np.array_equal(res["embed"], tok[300].astype(np.float32))
+    Kc = [np.zeros((64, kvd)) for _ in range(c.n_layers)]
+    Vc = [np.zeros((64, kvd)) for _ in range(c.n_layers)]
+    for pos, t in enumerate((41, 7, 300)):
+        x = tok[t]
+        for i, W in enumerate(Ws):
+            n1 = R.rmsnorm(x, W["attn_norm"], 1e-5)
+            h, x2 = R.decoder_layer(x, W, pos, Kc[i], Vc[i], cfgd)
+            n2 = R.rmsnorm(h, W["ffn_norm"], 1e-5)
+            if pos == 2:
+                L = res["layers"][i]
+                assert np.array_equal(L["attn_out"], plain[i, 0])
+                assert np.array_equal(L["ffn_out"], plain[i, 1])
+                for name, ref in (("attn_norm", n1), ("attn_out", h), ("ffn_norm", n2), ("ffn_out", x2)):
+                    assert np.max(np.abs(L[name] - ref)) <= 2e-5 * np.abs(ref).max(), (i, name)
+                # the norm outputs are not the hidden states (a swapped read point fails here)
+                assert np.max(np.abs(L["attn_norm"] - h)) > 1e-3 * np.abs(h).max()
+            x = x2
+
+
 def test_multi_codebook_step_uses_codes(small):
     e = small
     c = e.cfg

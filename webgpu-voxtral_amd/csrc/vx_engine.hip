@@ -996,7 +996,7 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   aplace((void **)&e->normed, DIM * 4);
   aplace((void **)&e->logits, (size_t)cfg.vocab_size * 4);
   aplace((void **)&e->part, (size_t)NH * ATTN_SPLITS * (HD + 2) * 4);
-  aplace((void **)&e->layer_stage, (size_t)nl * 2 * DIM * 4);
+  aplace((void **)&e->layer_stage, (size_t)(nl * 4 + 1) * DIM * 4);
   aplace((void **)&e->pos, 4);
   aplace((void **)&e->frame, 4);
   aplace((void **)&e->sem_code, 4);
@@ -1269,29 +1269,64 @@ int vx_backbone_step(vx_engine *e, int32_t token, int32_t mode, const float *pre
   return VX_OK;
 }
 
-int vx_backbone_step_layers(vx_engine *e, int32_t token, int32_t mode, const float *pre,
-                            float *layer_out) {
-  if (!e || !layer_out) return VX_E_INVALID;
+// One eager step that stages the reference's per-layer read points
+// (src/engine.ts:2106-2287) in layer_stage: the embedding (the first
+// layer's input) in row 0, then per layer attn_norm, attn_out, ffn_norm,
+// ffn_out.  The GEMVs fuse their RMSNorm, so the two norm outputs are
+// formed here by the final-norm kernel with the layer's gains: the fused
+// prologue's formula x * (1 / sqrt(sum x^2 / dim + eps)) * w, its sum of
+// squares added in another order.
+static int debug_layers_step(vx_engine *e, int32_t token, int32_t mode, const float *pre) {
   int rc = check_ready(e);
   if (rc) return rc;
   if ((rc = prepare_input(e, token, mode, pre))) return rc;
+  const float eps = e->cfg.norm_eps;
+  auto stage = [&](int row) { return e->layer_stage + (size_t)row * DIM; };
+  HIPCHK(e, hipMemcpyAsync(stage(0), e->x, DIM * 4, hipMemcpyDeviceToDevice, e->st));
   for (int l = 0; l < e->cfg.n_layers; l++) {
+    const int r = 1 + 4 * l;
+    hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->L[l].attn_norm, eps,
+                       stage(r), nullptr);
     enqueue_layer(e, l, VX_KERNEL_QKV);
     enqueue_layer(e, l, VX_KERNEL_ATTN);
     enqueue_layer(e, l, VX_KERNEL_OPROJ);
-    HIPCHK(e, hipMemcpyAsync(e->layer_stage + (size_t)(2 * l) * DIM, e->x, DIM * 4,
-                             hipMemcpyDeviceToDevice, e->st));
+    HIPCHK(e, hipMemcpyAsync(stage(r + 1), e->x, DIM * 4, hipMemcpyDeviceToDevice, e->st));
+    hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->L[l].ffn_norm, eps,
+                       stage(r + 2), nullptr);
     enqueue_layer(e, l, VX_KERNEL_GATEUP);
     enqueue_layer(e, l, VX_KERNEL_DOWN);
-    HIPCHK(e, hipMemcpyAsync(e->layer_stage + (size_t)(2 * l + 1) * DIM, e->x, DIM * 4,
-                             hipMemcpyDeviceToDevice, e->st));
+    HIPCHK(e, hipMemcpyAsync(stage(r + 3), e->x, DIM * 4, hipMemcpyDeviceToDevice, e->st));
   }
-  hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->final_norm,
-                     e->cfg.norm_eps, e->normed, e->pos);
+  hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->final_norm, eps, e->normed,
+                     e->pos);
   LAUNCHCHK(e);
   e->host_pos++;
-  HIPCHK(e, hipMemcpyAsync(layer_out, e->layer_stage, (size_t)e->cfg.n_layers * 2 * DIM * 4,
-                           hipMemcpyDeviceToHost, e->st));
+  return VX_OK;
+}
+
+int vx_backbone_step_layers(vx_engine *e, int32_t token, int32_t mode, const float *pre,
+                            float *layer_out) {
+  if (!e || !layer_out) return VX_E_INVALID;
+  int rc = debug_layers_step(e, token, mode, pre);
+  if (rc) return rc;
+  for (int l = 0; l < e->cfg.n_layers; l++)
+    for (int k = 0; k < 2; k++)
+      HIPCHK(e, hipMemcpyAsync(layer_out + (size_t)(2 * l + k) * DIM,
+                               e->layer_stage + (size_t)(2 + 4 * l + 2 * k) * DIM, DIM * 4,
+                               hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
+int vx_debug_backbone_layers(vx_engine *e, int32_t token, int32_t mode, const float *pre, float *embed,
+                             float *layers) {
+  if (!e || (!embed && !layers)) return VX_E_INVALID;
+  int rc = debug_layers_step(e, token, mode, pre);
+  if (rc) return rc;
+  if (embed) HIPCHK(e, hipMemcpyAsync(embed, e->layer_stage, DIM * 4, hipMemcpyDeviceToHost, e->st));
+  if (layers)
+    HIPCHK(e, hipMemcpyAsync(layers, e->layer_stage + DIM, (size_t)e->cfg.n_layers * 4 * DIM * 4,
+                             hipMemcpyDeviceToHost, e->st));
   HIPCHK(e, hipStreamSynchronize(e->st));
   return VX_OK;
 }

@@ -57,6 +57,17 @@ export declare class VoxtralEngine {
   debugRead(bufferName: string, count?: number): Promise<Float32Array>;
   backboneStepAndRead(tokenId: number, useAudioEmbedding?: boolean): Promise<number>;
   debugBackboneStepFull(tokenId: number, useAudioEmbedding?: boolean): Promise<Float32Array>;
+  debugBackboneLayerByLayer(tokenId: number): Promise<{
+    embed: Float32Array;
+    layers: Array<{
+      attn_norm: Float32Array;
+      attn_out: Float32Array;
+      ffn_norm: Float32Array;
+      ffn_out: Float32Array;
+    }>;
+    final_norm: Float32Array;
+    hidden: Float32Array;
+  }>;
   backboneStepEmbedding(embedding: Float32Array): Promise<Float32Array>;
   debugFMStep(debugNoise?: Float32Array): Promise<{
     semantic_logits: Float32Array;

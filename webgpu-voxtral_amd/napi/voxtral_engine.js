@@ -143,6 +143,25 @@ class VoxtralEngine {
     return native.backboneStep(this._handle(), tokenId, mode, null, false).normed;
   }
 
+  /** debugBackboneLayerByLayer(tokenId), src/engine.ts:2106-2287: one step
+   *  with the embedding, each layer's attn_norm, attn_out (after the
+   *  attention residual), ffn_norm and ffn_out (after the FFN residual),
+   *  the final norm and the last hidden state */
+  async debugBackboneLayerByLayer(tokenId) {
+    const h = this._handle();
+    const r = native.backboneLayers(h, tokenId, EMBED_TOKEN, null);
+    const dim = r.embed.length, n = r.layers.length / (4 * dim);
+    const at = (l, k) => r.layers.slice((4 * l + k) * dim, (4 * l + k + 1) * dim);
+    const layers = [];
+    for (let l = 0; l < n; l++) {
+      layers.push({ attn_norm: at(l, 0), attn_out: at(l, 1), ffn_norm: at(l, 2), ffn_out: at(l, 3) });
+    }
+    return {
+      embed: r.embed, layers, final_norm: native.read(h, 'normed', dim),
+      hidden: layers[n - 1].ffn_out.slice(),
+    };
+  }
+
   /** backbone step on a precomputed embedding (src/engine.ts:847-854) */
   async backboneStepEmbedding(embedding) {
     return native.backboneStep(this._handle(), 0, EMBED_PRECOMPUTED, embedding, false).normed;

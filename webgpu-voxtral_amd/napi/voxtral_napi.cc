@@ -57,6 +57,7 @@ struct EngineHandle {
   vx_engine *e = nullptr;
   bool busy = false;       // a generate() is running on the worker thread
   bool destroyed = false;  // destroy() was called
+  int n_layers = 0;        // backbone layers of the engine's config
 };
 
 void handle_finalize(napi_env, void *data, void *) {
@@ -213,6 +214,7 @@ napi_value create(napi_env env, napi_callback_info info) {
   if (rc) return throw_vx(env, nullptr, rc);
   auto *eh = new EngineHandle();
   eh->e = e;
+  eh->n_layers = c.n_layers;
   napi_value h;
   if (napi_create_external(env, eh, handle_finalize, nullptr, &h) != napi_ok) {
     vx_destroy(e);
@@ -457,6 +459,41 @@ napi_value backbone_step(napi_env env, napi_callback_info info) {
   napi_create_object(env, &out);
   set_int(env, out, "argmax", am);
   napi_set_named_property(env, out, "normed", new_f32(env, normed.data(), normed.size()));
+  return out;
+}
+
+// backboneLayers(h, token, embedMode, precomputed Float32Array|null)
+//   -> {embed: Float32Array(3072), layers: Float32Array(nLayers * 4 * 3072)}
+// (per layer attn_norm, attn_out, ffn_norm, ffn_out: the read points of
+// debugBackboneLayerByLayer)
+napi_value backbone_layers(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a) || a.n < 4) return nullptr;
+  EngineHandle *h = handle_of(env, a.v[0]);
+  if (!h) return nullptr;
+  vx_engine *e = handle(env, a.v[0]);
+  if (!e) return nullptr;
+  const float *pre = nullptr;
+  if (!is_nullish(env, a.v[3])) {
+    size_t n = 0;
+    pre = (const float *)typed(env, a.v[3], napi_float32_array, &n);
+    if (!pre) return nullptr;
+    if (n < 3072) {
+      napi_throw_range_error(env, nullptr, "precomputed embedding needs 3072 values");
+      return nullptr;
+    }
+  }
+  double tok = 0, mode = 0;
+  if (!int_arg(env, a.v[1], kI32Min, kI32Max, "tokenId", 0, &tok) ||
+      !int_arg(env, a.v[2], kI32Min, kI32Max, "embedMode", 0, &mode))
+    return nullptr;
+  std::vector<float> embed(3072), layers((size_t)h->n_layers * 4 * 3072);
+  int rc = vx_debug_backbone_layers(e, (int32_t)tok, (int32_t)mode, pre, embed.data(), layers.data());
+  if (rc) return throw_vx(env, e, rc);
+  napi_value out;
+  napi_create_object(env, &out);
+  napi_set_named_property(env, out, "embed", new_f32(env, embed.data(), embed.size()));
+  napi_set_named_property(env, out, "layers", new_f32(env, layers.data(), layers.size()));
   return out;
 }
 
@@ -818,6 +855,7 @@ napi_value init(napi_env env, napi_value exports) {
              {"reset", reset},
              {"position", position},
              {"backboneStep", backbone_step},
+             {"backboneLayers", backbone_layers},
              {"fmForward", fm_forward},
              {"setSemanticCode", set_semantic_code},
              {"read", read},

@@ -98,6 +98,7 @@ _SIGS = {
     "vx_set_position": (_I32, [_VP, _I32]),
     "vx_backbone_step": (_I32, [_VP, _I32, _I32, _VP, _I32, _VP, _VP]),
     "vx_backbone_step_layers": (_I32, [_VP, _I32, _I32, _VP, _VP]),
+    "vx_debug_backbone_layers": (_I32, [_VP, _I32, _I32, _VP, _VP, _VP]),
     "vx_fm_forward": (_I32, [_VP, _VP, _VP, _VP, _VP]),
     "vx_set_semantic_code": (_I32, [_VP, ctypes.c_uint32]),
     "vx_set_acoustic_codes": (_I32, [_VP, _VP]),
@@ -339,17 +340,34 @@ class VoxtralEngine:
         """debugBackboneStepFull (:2348-2357): final-norm hidden state."""
         return self.backbone_step(token_id, EMBED_AUDIO if use_audio_embedding else EMBED_TOKEN)[1]
 
-    def debug_backbone_layer_by_layer(self, token_id, precomputed=None):
-        """debugBackboneLayerByLayer (:2106-2287) read points: hidden after
-        each attention residual and after each FFN residual, + final norm."""
+    def debug_backbone_layer_by_layer(self, token_id, precomputed=None, use_audio_embedding=False):
+        """debugBackboneLayerByLayer (:2106-2287): the embedding, per layer
+        attn_norm, attn_out (hidden after the attention residual), ffn_norm
+        and ffn_out (hidden after the FFN residual), the final norm and the
+        last hidden state."""
+        c = self.config
+        emb = np.empty(c.dim, np.float32)
+        out = np.empty((c.n_layers, 4, c.dim), np.float32)
+        pre = _f32(precomputed, c.dim) if precomputed is not None else None
+        mode = EMBED_PRECOMPUTED if pre is not None else (EMBED_AUDIO if use_audio_embedding else EMBED_TOKEN)
+        self._check(self._lib.vx_debug_backbone_layers(self._h, int(token_id), mode, _ptr(pre),
+                                                       emb.ctypes.data, out.ctypes.data))
+        names = ("attn_norm", "attn_out", "ffn_norm", "ffn_out")
+        return {"embed": emb,
+                "layers": [{n: out[i, k] for k, n in enumerate(names)} for i in range(c.n_layers)],
+                "final_norm": self.debug_read("normed", c.dim), "hidden": out[-1, 3].copy()}
+
+    def backbone_step_layers(self, token_id, mode=EMBED_TOKEN, precomputed=None):
+        """Hidden state after each attention and each FFN residual,
+        [n_layers][2][dim] (vx_backbone_step_layers)."""
         c = self.config
         out = np.empty((c.n_layers, 2, c.dim), np.float32)
         pre = _f32(precomputed, c.dim) if precomputed is not None else None
-        mode = EMBED_PRECOMPUTED if pre is not None else EMBED_TOKEN
+        if pre is not None:
+            mode = EMBED_PRECOMPUTED
         self._check(self._lib.vx_backbone_step_layers(self._h, int(token_id), mode, _ptr(pre),
                                                       out.ctypes.data))
-        return {"layers": [{"attn_out": out[i, 0], "ffn_out": out[i, 1]} for i in range(c.n_layers)],
-                "final_norm": self.debug_read("normed", c.dim), "hidden": out[-1, 1]}
+        return out
 
     # -- FM (fmForward :1240-1380) --
     def debug_fm_step(self, debug_noise=None):
