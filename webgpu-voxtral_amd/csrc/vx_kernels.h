@@ -1515,6 +1515,8 @@ __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
   for (int j = 0; j < NAC / 4; j++) wr[j] = ((const uint2 *)(a.w_in + (size_t)row * NAC))[j];
   const float tp = a.tproj[row], lp = a.llm[row];
   const float g = h2f(a.gn[row]);
+  // x_{s-1} too, so that no load waits behind the velocity's barrier
+  const float xprev = a.step > 0 && t < NAC ? a.xh[(a.step - 1) * NAC + t] : 0.f;
   if (a.step > 0) {
     fm_velocity(a.ac_part, a.ac_ssq, vs);
     if (blockIdx.x == 0 && t < 2 * NAC) a.vel[(size_t)(a.step - 1) * 2 * NAC + t] = vs[t];
@@ -1524,7 +1526,7 @@ __global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
     if (a.step == 0) {
       x = a.noise ? a.noise[t] : fm_gauss(*a.noise_seed, a.noise_stream, (uint64_t)(*a.frame) * NAC + t);
     } else {
-      x = cfg_euler(a.xh[(a.step - 1) * NAC + t], vs[t], vs[NAC + t], a.alpha, a.dt);
+      x = cfg_euler(xprev, vs[t], vs[NAC + t], a.alpha, a.dt);
     }
     xs[t] = x;
     if (blockIdx.x == 0) a.xh[a.step * NAC + t] = x;
@@ -1597,10 +1599,11 @@ __global__ __launch_bounds__(256) void fm_finish_kernel(float *xh, float *vel, c
                                                        uint32_t *codes, int levels, int *frame_counter) {
   __shared__ float vs[2 * NAC];
   const int t = threadIdx.x;
+  const float xprev = t < NAC ? xh[last * NAC + t] : 0.f;  // issued before the velocity's barrier
   fm_velocity(ac_part, ac_ssq, vs);
   if (t < 2 * NAC) vel[(size_t)last * 2 * NAC + t] = vs[t];
   if (t < NAC) {
-    float x = cfg_euler(xh[last * NAC + t], vs[t], vs[NAC + t], alpha, dt);
+    float x = cfg_euler(xprev, vs[t], vs[NAC + t], alpha, dt);
     xh[(last + 1) * NAC + t] = x;
     float c = fminf(fmaxf(x, -1.0f), 1.0f);
     float top = (float)(levels - 1);
