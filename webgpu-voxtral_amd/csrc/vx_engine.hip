@@ -214,7 +214,7 @@ void launch_gemv(hipStream_t st, const GemvArgs &a) {
   constexpr int units = WAVES * (EPI == EPI_SWIGLU ? RPW / 2 : RPW);
   const int grid = (a.M + units - 1) / units;
   hipLaunchKernelGGL((gemv_kernel<NB, WAVES, RPW, EPI, NORM, K, KT>), dim3(grid),
-                     dim3(WAVES * 64), 0, st, a);
+                     dim3(WAVES * 64), 0, st, a.W, a.W2, a.x, a.norm_w, a.out, a);
 }
 
 GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, int M) {
@@ -239,7 +239,7 @@ GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, in
 template <int EPI, int K, int RG, int KS, int P, bool KEEP = false>
 void launch_gemm6(hipStream_t st, const Gemm6Args &a, int rows) {
   hipLaunchKernelGGL((gemm6_kernel<EPI, K, RG, KS, P, KEEP>), dim3(rows / (FTR * RG)), dim3(RG * KS * 64),
-                     0, st, a);
+                     0, st, a.W, a.W2, a.B, a.ssq, a.out, a);
 }
 // Launch shapes of the four FM GEMMs <RG, KS, P>, picked on the whole frame
 // loop.  A build with -DVX_FM_SWEEP selects each from a candidate list by
@@ -295,7 +295,7 @@ template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K, int D = 2>
 void launch_gemv1(hipStream_t st, const GemvArgs &a) {
   constexpr int per_block = WAVES * UPW;
   hipLaunchKernelGGL((gemv1_kernel<WAVES, UPW, UPG, EPI, NORM, K, D>), dim3(a.M / per_block),
-                     dim3(WAVES * 64), 0, st, a);
+                     dim3(WAVES * 64), 0, st, a.W, a.W2, a.x, a.norm_w, a.out, a);
 }
 // unit counts of the backbone GEMVs must split into whole blocks
 static_assert((QKV_ROWS / 2) % 6 == 0 && DIM % 4 == 0 && HID % 12 == 0 && DIM % 6 == 0,
@@ -322,9 +322,11 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
   if (only < 0 || only == VX_KERNEL_ATTN) {
     AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn};
     if (e->kv_f32)
-      hipLaunchKernelGGL(attn_partial_kernel<float>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(attn_partial_kernel<float>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a.pos, a.kc,
+                         a.vc, a.q, a);
     else
-      hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a);
+      hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a.pos, a.kc,
+                         a.vc, a.q, a);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->pos, e->attn);
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
@@ -499,7 +501,8 @@ static void enqueue_fm_step_in(vx_engine *e, int s, const float *noise_src, int 
                 e->fm_b_attn, e->FL[0].attn_norm, e->fm_ssq_attn,
                 e->sem_logits, sem_mask, e->sem_code};
   const bool argmax = s == 0 && sem_mask >= 0;
-  hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256 + (argmax ? 1 : 0)), dim3(256), 0, e->st, fa);
+  hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256 + (argmax ? 1 : 0)), dim3(256), 0, e->st, fa.w_in,
+                     fa.ac_part, fa.ac_ssq, (const float *)fa.xh, fa);
 }
 
 // fmForward with CFG batched: 6 vectors (2 branches x 3 positions) share

@@ -232,7 +232,15 @@ __device__ __forceinline__ void kv_store2(void *cache, int kv_f32, int max_seq, 
 // row covering columns [c*512 + lane*8, +8), so a wave reads 1 KB of one
 // row per load instruction.
 template <int NB, int WAVES, int RPW, int EPI, bool NORM, int K, int KT>
-__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint16_t *W, const uint16_t *W2, const float *x,
+                                                         const uint16_t *norm_w, float *out, GemvArgs args) {
+  // leading pointer arguments: preloaded into SGPRs (as in gemv1_kernel)
+  GemvArgs a = args;
+  a.W = W;
+  a.W2 = W2;
+  a.x = x;
+  a.norm_w = norm_w;
+  a.out = out;
   static_assert(KT == K && K % 512 == 0 && EPI != EPI_QKV_ROPE, "one K tile");
   constexpr int NT = WAVES * 64;
   constexpr int NCH = K / 512;
@@ -439,7 +447,17 @@ __device__ __forceinline__ void unit_epilogue(const GemvArgs &a, int unit, const
 }
 
 template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K, int D>
-__global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(GemvArgs a) {
+__global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(const uint16_t *W, const uint16_t *W2, const float *x,
+                                                          const uint16_t *norm_w, float *out, GemvArgs args) {
+  // the pointers the first loads need arrive as leading scalar arguments,
+  // which the hardware preloads into SGPRs at wave launch (no kernel-
+  // argument load before the first weight load)
+  GemvArgs a = args;
+  a.W = W;
+  a.W2 = W2;
+  a.x = x;
+  a.norm_w = norm_w;
+  a.out = out;
   constexpr int RU = rows_per_unit<EPI>();
   constexpr int RG = UPG * RU;  // rows per group
   constexpr int NCH = K / 512;
@@ -606,7 +624,15 @@ __device__ __forceinline__ float2 vpair(const uint16_t *v) {
 // softmax update, then lane l accumulates P.V for dims 2l, 2l+1.  The next
 // tile's loads are in flight while the current one is computed.
 template <typename KVT>
-__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const void *kc, const void *vc,
+                                                           const float *q, AttnArgs args) {
+  // the position, cache and query pointers arrive preloaded in SGPRs: the
+  // position load, and the tile loads behind it, wait on no argument load
+  AttnArgs a = args;
+  a.pos = pos;
+  a.kc = kc;
+  a.vc = vc;
+  a.q = q;
   using G = KvTile<KVT>;
   const int split = blockIdx.x, kvh = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -1022,7 +1048,15 @@ struct Gemm6Args {
 // k-slices are summed through LDS.  Grid = rows / (FTR RG).  KEEP: plain
 // weight loads (cached in L2) instead of non-temporal ones.
 template <int EPI, int K, int RG, int KS, int P, bool KEEP = false>
-__global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(Gemm6Args a) {
+__global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(const uint16_t *W, const uint16_t *W2, const h8 *B,
+                                                            const float *ssq, float *out, Gemm6Args args) {
+  // the operands of the first loads arrive preloaded in SGPRs
+  Gemm6Args a = args;
+  a.W = W;
+  a.W2 = W2;
+  a.B = B;
+  a.ssq = ssq;
+  a.out = out;
   constexpr int TL = EPI == EPI_SWIGLU ? 2 : 1;
   constexpr int NC = K / 32, NCW = NC / KS;
   static_assert(NC % KS == 0 && NCW % P == 0, "shape");
@@ -1499,7 +1533,14 @@ __device__ __forceinline__ void fm_velocity(const float *ac_part, const float *a
 // Start of Euler step s: x_s (from x_{s-1} and the CFG velocity of step
 // s-1, or the noise at s=0), x_t_proj = input_projection(x_s), and both CFG
 // sequences [x_t_proj, time_proj, llm | 0] (src/engine.ts:1292-1349).
-__global__ __launch_bounds__(256) void fm_step_in_kernel(FmStepArgs a) {
+__global__ __launch_bounds__(256) void fm_step_in_kernel(const uint16_t *w_in, const float *ac_part,
+                                                         const float *ac_ssq, const float *xh, FmStepArgs args) {
+  // the first loads' pointers arrive preloaded in SGPRs
+  FmStepArgs a = args;
+  a.w_in = w_in;
+  a.ac_part = ac_part;
+  a.ac_ssq = ac_ssq;
+  a.xh = (float *)xh;
   __shared__ float xs[NAC];
   __shared__ float vs[2 * NAC];
   const int t = threadIdx.x;
