@@ -253,14 +253,14 @@ static int fm_sweep_pick(const char *name, int n) {
 }
 #define FM_PICK(list, name) list[fm_sweep_pick(name, (int)(sizeof(list) / sizeof(list[0])))]
 static const Gemm6Launch kFmQkv[] = {
-    launch_gemm6<EPI_QKV, DIM, 1, 8, 4>,  launch_gemm6<EPI_QKV, DIM, 1, 8, 6>,
-    launch_gemm6<EPI_QKV, DIM, 1, 8, 12>, launch_gemm6<EPI_QKV, DIM, 1, 4, 8>,
+    launch_gemm6<EPI_QKV, DIM, 1, 4, 8>,  launch_gemm6<EPI_QKV, DIM, 1, 8, 6>,
+    launch_gemm6<EPI_QKV, DIM, 1, 8, 12>, launch_gemm6<EPI_QKV, DIM, 1, 8, 4>,
     launch_gemm6<EPI_QKV, DIM, 1, 4, 12>, launch_gemm6<EPI_QKV, DIM, 1, 6, 8>,
     launch_gemm6<EPI_QKV, DIM, 1, 12, 8>, launch_gemm6<EPI_QKV, DIM, 1, 16, 6>,
     launch_gemm6<EPI_QKV, DIM, 2, 4, 6>,  launch_gemm6<EPI_QKV, DIM, 2, 8, 4>};
 static const Gemm6Launch kFmO[] = {
-    launch_gemm6<EPI_RESID, QD, 1, 16, 4>, launch_gemm6<EPI_RESID, QD, 1, 16, 8>,
-    launch_gemm6<EPI_RESID, QD, 1, 8, 8>,  launch_gemm6<EPI_RESID, QD, 1, 8, 16>,
+    launch_gemm6<EPI_RESID, QD, 1, 8, 16>, launch_gemm6<EPI_RESID, QD, 1, 16, 8>,
+    launch_gemm6<EPI_RESID, QD, 1, 8, 8>,  launch_gemm6<EPI_RESID, QD, 1, 16, 4>,
     launch_gemm6<EPI_RESID, QD, 2, 8, 8>,  launch_gemm6<EPI_RESID, QD, 1, 4, 16>,
     launch_gemm6<EPI_RESID, QD, 1, 16, 2>, launch_gemm6<EPI_RESID, QD, 2, 4, 16>};
 static const Gemm6Launch kFmGateUp[] = {
@@ -275,13 +275,17 @@ static const Gemm6Launch kFmDown[] = {
     launch_gemm6<EPI_RESID, HID, 1, 16, 9>,  launch_gemm6<EPI_RESID, HID, 1, 16, 18>,
     launch_gemm6<EPI_RESID, HID, 1, 6, 16>,  launch_gemm6<EPI_RESID, HID, 1, 6, 24>,
     launch_gemm6<EPI_RESID, HID, 1, 9, 16>,  launch_gemm6<EPI_RESID, HID, 1, 4, 24>};
+static const Gemm6Launch kFmO0[] = {launch_gemm6<EPI_RESID, QD, 1, 8, 16, true>,
+                                     launch_gemm6<EPI_RESID, QD, 1, 16, 4, true>};
 #define FM_GEMM_QKV FM_PICK(kFmQkv, "VX_FM_QKV")
 #define FM_GEMM_O FM_PICK(kFmO, "VX_FM_O")
+#define FM_GEMM_O_KEEP FM_PICK(kFmO0, "VX_FM_O0")
 #define FM_GEMM_GATEUP FM_PICK(kFmGateUp, "VX_FM_GATEUP")
 #define FM_GEMM_DOWN FM_PICK(kFmDown, "VX_FM_DOWN")
 #else
-#define FM_GEMM_QKV (launch_gemm6<EPI_QKV, DIM, 1, 8, 4>)
-#define FM_GEMM_O (launch_gemm6<EPI_RESID, QD, 1, 16, 4>)
+#define FM_GEMM_QKV (launch_gemm6<EPI_QKV, DIM, 1, 4, 8>)
+#define FM_GEMM_O (launch_gemm6<EPI_RESID, QD, 1, 8, 16>)
+#define FM_GEMM_O_KEEP (launch_gemm6<EPI_RESID, QD, 1, 8, 16, true>)
 #define FM_GEMM_GATEUP (launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 16>)
 #define FM_GEMM_DOWN (launch_gemm6<EPI_RESID, HID, 1, 12, 12>)
 #endif
@@ -446,7 +450,7 @@ static void enqueue_fm_kernel(vx_engine *e, int l, int k, int nssq_attn) {
       // step (6.3 against 7.5 us per launch); every other weight stream is
       // non-temporal.  Only one FM matrix fits.
       if (l == 0)
-        launch_gemm6<EPI_RESID, QD, 1, 16, 4, true>(st, a, DIM);
+        FM_GEMM_O_KEEP(st, a, DIM);
       else
         FM_GEMM_O(st, a, DIM);
       break;
