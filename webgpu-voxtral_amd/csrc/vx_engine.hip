@@ -301,8 +301,41 @@ void launch_gemv1(hipStream_t st, const GemvArgs &a) {
   hipLaunchKernelGGL((gemv1_kernel<WAVES, UPW, UPG, EPI, NORM, K, D>), dim3(a.M / per_block),
                      dim3(WAVES * 64), 0, st, a.W, a.W2, a.x, a.norm_w, a.out, a);
 }
+// Backbone GEMV launch shapes (waves per block, one unit per wave).  A build
+// with -DVX_BB_SWEEP selects each from a candidate list by the environment
+// (VX_BB_QKV, VX_BB_O, VX_BB_GATEUP, VX_BB_DOWN = index).
+#ifdef VX_BB_SWEEP
+typedef void (*GemvLaunch)(hipStream_t, const GemvArgs &);
+static int bb_sweep_pick(const char *name, int n) {
+  const char *v = getenv(name);
+  const int i = v ? atoi(v) : 0;
+  return i < 0 || i >= n ? 0 : i;
+}
+#define BB_PICK(list, name) list[bb_sweep_pick(name, (int)(sizeof(list) / sizeof(list[0])))]
+static const GemvLaunch kBbQkv[] = {
+    launch_gemv1<6, 1, 1, EPI_QKV_ROPE, true, DIM, 1>, launch_gemv1<4, 1, 1, EPI_QKV_ROPE, true, DIM, 1>,
+    launch_gemv1<8, 1, 1, EPI_QKV_ROPE, true, DIM, 1>, launch_gemv1<12, 1, 1, EPI_QKV_ROPE, true, DIM, 1>};
+static const GemvLaunch kBbO[] = {
+    launch_gemv1<12, 1, 1, EPI_RESID, false, QD, 1>, launch_gemv1<6, 1, 1, EPI_RESID, false, QD, 1>,
+    launch_gemv1<8, 1, 1, EPI_RESID, false, QD, 1>, launch_gemv1<4, 1, 1, EPI_RESID, false, QD, 1>};
+static const GemvLaunch kBbGateUp[] = {
+    launch_gemv1<12, 1, 1, EPI_SWIGLU, true, DIM, 1>, launch_gemv1<8, 1, 1, EPI_SWIGLU, true, DIM, 1>,
+    launch_gemv1<16, 1, 1, EPI_SWIGLU, true, DIM, 1>};
+static const GemvLaunch kBbDown[] = {
+    launch_gemv1<6, 1, 1, EPI_RESID, false, HID, 1>, launch_gemv1<4, 1, 1, EPI_RESID, false, HID, 1>,
+    launch_gemv1<8, 1, 1, EPI_RESID, false, HID, 1>, launch_gemv1<12, 1, 1, EPI_RESID, false, HID, 1>};
+#define BB_GEMV_QKV BB_PICK(kBbQkv, "VX_BB_QKV")
+#define BB_GEMV_O BB_PICK(kBbO, "VX_BB_O")
+#define BB_GEMV_GATEUP BB_PICK(kBbGateUp, "VX_BB_GATEUP")
+#define BB_GEMV_DOWN BB_PICK(kBbDown, "VX_BB_DOWN")
+#else
+#define BB_GEMV_QKV (launch_gemv1<6, 1, 1, EPI_QKV_ROPE, true, DIM, 1>)
+#define BB_GEMV_O (launch_gemv1<12, 1, 1, EPI_RESID, false, QD, 1>)
+#define BB_GEMV_GATEUP (launch_gemv1<12, 1, 1, EPI_SWIGLU, true, DIM, 1>)
+#define BB_GEMV_DOWN (launch_gemv1<6, 1, 1, EPI_RESID, false, HID, 1>)
+#endif
 // unit counts of the backbone GEMVs must split into whole blocks
-static_assert((QKV_ROWS / 2) % 6 == 0 && DIM % 4 == 0 && HID % 12 == 0 && DIM % 6 == 0,
+static_assert((QKV_ROWS / 2) % 6 == 0 && DIM % 12 == 0 && HID % 12 == 0 && DIM % 6 == 0,
               "launch shapes");
 
 // One backbone layer: 6 launches (norm + QKV + rope + KV write | attention
@@ -321,7 +354,7 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
     a.kv_f32 = e->kv_f32;
     a.max_seq = e->max_seq;
     a.inv_freq = e->inv_freq;
-    launch_gemv1<6, 1, 1, EPI_QKV_ROPE, true, DIM, 1>(st, a);
+    BB_GEMV_QKV(st, a);
   }
   if (only < 0 || only == VX_KERNEL_ATTN) {
     AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn};
@@ -335,18 +368,18 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
     GemvArgs a = gargs(W.wo, e->attn, QD, e->x, 0, DIM);
-    launch_gemv1<4, 1, 1, EPI_RESID, false, QD, 1>(st, a);
+    BB_GEMV_O(st, a);
   }
   if (only < 0 || only == VX_KERNEL_GATEUP) {
     GemvArgs a = gargs(W.w1, e->x, DIM, e->act, 0, HID);
     a.W2 = W.w3;
     a.norm_w = W.ffn_norm;
     a.eps = e->cfg.norm_eps;
-    launch_gemv1<12, 1, 1, EPI_SWIGLU, true, DIM, 1>(st, a);
+    BB_GEMV_GATEUP(st, a);
   }
   if (only < 0 || only == VX_KERNEL_DOWN) {
     GemvArgs a = gargs(W.w2, e->act, HID, e->x, 0, DIM);
-    launch_gemv1<6, 1, 1, EPI_RESID, false, HID, 1>(st, a);
+    BB_GEMV_DOWN(st, a);
   }
 }
 
