@@ -539,7 +539,7 @@ static void enqueue_fm_step_in(vx_engine *e, int s, const float *noise_src, int 
                 e->sem_logits, sem_mask, e->sem_code};
   const bool argmax = s == 0 && sem_mask >= 0;
   hipLaunchKernelGGL(fm_step_in_kernel, dim3(DIM / 256 + (argmax ? 1 : 0)), dim3(256), 0, e->st, fa.w_in,
-                     fa.ac_part, fa.ac_ssq, (const float *)fa.xh, fa);
+                     fa.ac_part, fa.ac_ssq, fa.xh, fa);
 }
 
 // fmForward with CFG batched: 6 vectors (2 branches x 3 positions) share

@@ -1534,13 +1534,13 @@ __device__ __forceinline__ void fm_velocity(const float *ac_part, const float *a
 // s-1, or the noise at s=0), x_t_proj = input_projection(x_s), and both CFG
 // sequences [x_t_proj, time_proj, llm | 0] (src/engine.ts:1292-1349).
 __global__ __launch_bounds__(256) void fm_step_in_kernel(const uint16_t *w_in, const float *ac_part,
-                                                         const float *ac_ssq, const float *xh, FmStepArgs args) {
+                                                         const float *ac_ssq, float *xh, FmStepArgs args) {
   // the first loads' pointers arrive preloaded in SGPRs
   FmStepArgs a = args;
   a.w_in = w_in;
   a.ac_part = ac_part;
   a.ac_ssq = ac_ssq;
-  a.xh = (float *)xh;
+  a.xh = xh;
   __shared__ float xs[NAC];
   __shared__ float vs[2 * NAC];
   const int t = threadIdx.x;
