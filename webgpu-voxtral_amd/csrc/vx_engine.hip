@@ -132,7 +132,8 @@ struct vx_engine {
   uint64_t *rng_state = nullptr;
   double *tp_params = nullptr;
   float *tp_logits = nullptr;
-  uint32_t *h_frame = nullptr;  // [2][1 + NAC]
+  uint32_t *h_frame = nullptr;  // [2][1 + NAC], pinned, written by the frame's last kernels
+  uint32_t *d_frame = nullptr;  // h_frame's device address
   hipEvent_t ev_frame[2] = {nullptr, nullptr};
   hipGraphExec_t fm_topp_exec = nullptr, frame_topp_exec = nullptr;
 
@@ -566,7 +567,8 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
     // kernel, and for the last step by fm_finish
   }
   hipLaunchKernelGGL(fm_finish_kernel, dim3(1), dim3(256), 0, st, e->xh, e->vel, e->ac_part, e->ac_ssq,
-                     e->nsteps() - 1, alpha, dt, e->codes, e->cfg.acoustic_levels, e->frame);
+                     e->nsteps() - 1, alpha, dt, e->codes, e->cfg.acoustic_levels, e->frame, e->sem_code,
+                     e->d_frame);
 }
 
 // ------------------------------------------------------------------ graphs
@@ -591,7 +593,7 @@ static void fm_plain_body(vx_engine *e) { enqueue_fm(e, nullptr, false); }
 static void fm_topp_body(vx_engine *e) {
   fm_plain_body(e);
   hipLaunchKernelGGL(topp_sample_kernel, dim3(1), dim3(TP_NT), 0, e->st, e->sem_logits, SEMV, 8194,
-                     e->tp_params, e->rng_state, e->sem_code);
+                     e->tp_params, e->rng_state, e->sem_code, e->frame, e->d_frame);
 }
 static void frame_body(vx_engine *e) {
   hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
@@ -787,7 +789,12 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   (void)hipEventCreate(&e->ev1);
   (void)hipEventCreateWithFlags(&e->ev_frame[0], hipEventDisableTiming);
   (void)hipEventCreateWithFlags(&e->ev_frame[1], hipEventDisableTiming);
-  if (hipHostMalloc((void **)&e->h_frame, 2 * (1 + NAC) * 4, hipHostMallocDefault) != hipSuccess) {
+  // coherent (uncached) pinned memory: the frame's codes are stored into it
+  // by fm_finish_kernel / topp_sample_kernel, visible to the host once the
+  // frame's event has completed
+  if (hipHostMalloc((void **)&e->h_frame, 2 * (1 + NAC) * 4, hipHostMallocMapped | hipHostMallocCoherent) !=
+          hipSuccess ||
+      hipHostGetDevicePointer((void **)&e->d_frame, e->h_frame, 0) != hipSuccess) {
     vx_destroy(e);
     return fail(nullptr, VX_E_NOMEM, "hipHostMalloc of readback slots failed");
   }
@@ -1770,7 +1777,7 @@ int vx_sample_top_p(vx_engine *e, const float *logits, int32_t n, int32_t valid,
   HIPCHK(e, hipMemcpyAsync(e->tp_params, params, 16, hipMemcpyHostToDevice, e->st));
   HIPCHK(e, hipMemcpyAsync(e->rng_state, state, 8, hipMemcpyHostToDevice, e->st));
   hipLaunchKernelGGL(topp_sample_kernel, dim3(1), dim3(TP_NT), 0, e->st, e->tp_logits, n, valid,
-                     e->tp_params, e->rng_state, e->argmax_res);
+                     e->tp_params, e->rng_state, e->argmax_res, (const int *)nullptr, (uint32_t *)nullptr);
   LAUNCHCHK(e);
   HIPCHK(e, hipMemcpyAsync(code, e->argmax_res, 4, hipMemcpyDeviceToHost, e->st));
   HIPCHK(e, hipMemcpyAsync(state, e->rng_state, 8, hipMemcpyDeviceToHost, e->st));
@@ -1807,7 +1814,7 @@ int vx_sample_top_p_noalloc(const float *logits, int32_t n, int32_t valid, doubl
   HIPCHK(nullptr, hipMemcpyAsync(d_params, params, sizeof params, hipMemcpyHostToDevice, st));
   HIPCHK(nullptr, hipMemcpyAsync(d_state, state, 8, hipMemcpyHostToDevice, st));
   hipLaunchKernelGGL(topp_sample_kernel, dim3(1), dim3(TP_NT), 0, st, d_logits, n, valid, d_params,
-                     d_state, d_code);
+                     d_state, d_code, (const int *)nullptr, (uint32_t *)nullptr);
   LAUNCHCHK(nullptr);
   HIPCHK(nullptr, hipMemcpyAsync(code, d_code, 4, hipMemcpyDeviceToHost, st));
   HIPCHK(nullptr, hipMemcpyAsync(state, d_state, 8, hipMemcpyDeviceToHost, st));
@@ -2167,12 +2174,12 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
     hipGraphExec_t *frame_slot = greedy ? &e->frame_exec : &e->frame_topp_exec;
     void (*fm_body)(vx_engine *) = greedy ? fm_greedy_body : fm_topp_body;
     void (*fr_body)(vx_engine *) = greedy ? frame_body : frame_topp_body;
+    // frame f's last kernels store its codes into host slot f & 1 (the
+    // device frame counter is f there: vx_reset zeroed it and each frame's
+    // fm_finish_kernel advances it), so the host only waits for its event
     auto enqueue_frame = [&](int f) -> int {
       int r = f == 0 ? run_seq(e, fm_slot, fm_body) : run_seq(e, frame_slot, fr_body);
       if (r) return r;
-      uint32_t *slot = e->h_frame + (f & 1) * (1 + NAC);
-      HIPCHK(e, hipMemcpyAsync(slot, e->sem_code, 4, hipMemcpyDeviceToHost, e->st));
-      HIPCHK(e, hipMemcpyAsync(slot + 1, e->codes, NAC * 4, hipMemcpyDeviceToHost, e->st));
       HIPCHK(e, hipEventRecord(e->ev_frame[f & 1], e->st));
       return VX_OK;
     };

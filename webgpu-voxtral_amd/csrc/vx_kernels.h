@@ -1286,9 +1286,12 @@ __device__ __forceinline__ uint64_t tp_mass(uint64_t key) {
   return (uint64_t)((double)q * 0x1p62);
 }
 
+// pub (or null): the frame's host-visible code slots [2][1 + NAC] (pinned
+// host memory); the code also goes to slot (*frame - 1) & 1, the slot
+// fm_finish_kernel filled for this frame before it advanced *frame.
 __global__ __launch_bounds__(TP_NT) void topp_sample_kernel(const float *logits, int n, int valid,
                                                             const double *params, uint64_t *rng,
-                                                            uint32_t *out) {
+                                                            uint32_t *out, const int *frame, uint32_t *pub) {
   const double top_p = params[0], temp = params[1];  // in device memory: graphs stay valid
   __shared__ uint64_t key[TP_MAXN];       // first holds s_i, then p_i, as floats
   __shared__ uint64_t bmass[TP_BINS];     // also the f64 tree of the p sum
@@ -1454,7 +1457,10 @@ __global__ __launch_bounds__(TP_NT) void topp_sample_kernel(const float *logits,
   __syncthreads();
   uint64_t kp = 0, dummy = 0;
   if (!select(target, kp, dummy)) select(0, kp, dummy);  // (t <= resum: not reached)
-  if (tid == 0) *out = (uint32_t)(kp & 0x3FFF);
+  if (tid == 0) {
+    *out = (uint32_t)(kp & 0x3FFF);
+    if (pub) pub[((*frame - 1) & 1) * (1 + NAC)] = (uint32_t)(kp & 0x3FFF);
+  }
 }
 
 // ------------------------------------------------------------- FM kernels
@@ -1634,13 +1640,20 @@ __global__ __launch_bounds__(64) void fm_attn_kernel(const float *q, const float
 
 // End of the Euler loop: last CFG/Euler update, then fsqQuantize (round
 // half to even) into the device acoustic codes; also advances the frame
-// counter of the noise generator.
+// counter of the noise generator.  pub (or null): host-visible code slots
+// [2][1 + NAC] in pinned host memory; the frame's acoustic codes and the
+// device semantic code go to slot frame & 1 (a later kernel may replace
+// the semantic code), so the host reads a frame's codes without a copy.
 __global__ __launch_bounds__(256) void fm_finish_kernel(float *xh, float *vel, const float *ac_part,
                                                        const float *ac_ssq, int last, float alpha, float dt,
-                                                       uint32_t *codes, int levels, int *frame_counter) {
+                                                       uint32_t *codes, int levels, int *frame_counter,
+                                                       const uint32_t *sem_code, uint32_t *pub) {
   __shared__ float vs[2 * NAC];
   const int t = threadIdx.x;
   const float xprev = t < NAC ? xh[last * NAC + t] : 0.f;  // issued before the velocity's barrier
+  // read before the barrier inside fm_velocity; thread 0 advances it after
+  const int fc = frame_counter ? *frame_counter : 0;
+  uint32_t *slot = pub ? pub + (fc & 1) * (1 + NAC) : nullptr;
   fm_velocity(ac_part, ac_ssq, vs);
   if (t < 2 * NAC) vel[(size_t)last * 2 * NAC + t] = vs[t];
   if (t < NAC) {
@@ -1649,8 +1662,11 @@ __global__ __launch_bounds__(256) void fm_finish_kernel(float *xh, float *vel, c
     float c = fminf(fmaxf(x, -1.0f), 1.0f);
     float top = (float)(levels - 1);
     float sc = rintf((c + 1.0f) * 0.5f * top);
-    codes[t] = (uint32_t)fminf(fmaxf(sc, 0.0f), top) + 2u;
+    const uint32_t code = (uint32_t)fminf(fmaxf(sc, 0.0f), top) + 2u;
+    codes[t] = code;
+    if (slot) slot[1 + t] = code;
   }
+  if (slot && t == NAC) slot[0] = *sem_code;
   if (t == 0 && frame_counter) *frame_counter += 1;
 }
 
