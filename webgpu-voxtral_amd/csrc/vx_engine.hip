@@ -295,6 +295,10 @@ static_assert(QKV_ROWS % (256 * FTR) == 0 && DIM % (256 * FTR) == 0 && HID % (25
                   DIM / FTR <= SSQ_MAX && DIM % 256 == 0,
               "FM GEMM tiles");
 
+// decode attention partials: (splits, KV heads), or one dimension when a KV
+// head's blocks are grouped on one XCD
+static dim3 attn_grid() { return VX_ATTN_XCD ? dim3(ATTN_SPLITS * NKV) : dim3(ATTN_SPLITS, NKV); }
+
 // Streaming GEMV launch: M units split exactly into blocks of WAVES*UPW.
 template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K, int D = 2>
 void launch_gemv1(hipStream_t st, const GemvArgs &a) {
@@ -360,10 +364,10 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
   if (only < 0 || only == VX_KERNEL_ATTN) {
     AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn};
     if (e->kv_f32)
-      hipLaunchKernelGGL(attn_partial_kernel<float>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a.pos, a.kc,
+      hipLaunchKernelGGL(attn_partial_kernel<float>, attn_grid(), dim3(256), 0, st, a.pos, a.kc,
                          a.vc, a.q, a);
     else
-      hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, dim3(ATTN_SPLITS, NKV), dim3(256), 0, st, a.pos, a.kc,
+      hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, attn_grid(), dim3(256), 0, st, a.pos, a.kc,
                          a.vc, a.q, a);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->pos, e->attn);
   }

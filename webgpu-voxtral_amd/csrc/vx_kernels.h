@@ -49,6 +49,11 @@ constexpr int SEMV = 8320;
 #ifndef VX_ATTN_LIVE_COMBINE
 #define VX_ATTN_LIVE_COMBINE 0
 #endif
+// one KV head's attention blocks on one XCD (see attn_partial_kernel); 0
+// keeps the 2-D (split, KV head) grid
+#ifndef VX_ATTN_XCD
+#define VX_ATTN_XCD 1
+#endif
 constexpr int ATTN_SPLITS = VX_ATTN_SPLITS;
 constexpr bool ATTN_TILE_ALIGN = VX_ATTN_TILE_ALIGN != 0;
 constexpr bool ATTN_LIVE_COMBINE = VX_ATTN_LIVE_COMBINE != 0;
@@ -634,7 +639,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const
   a.vc = vc;
   a.q = q;
   using G = KvTile<KVT>;
+#if VX_ATTN_XCD
+  // 1-D grid, block b = split * NKV + kv head: workgroups are dealt to the
+  // 8 XCDs round-robin, so a KV head's splits (and the combine blocks of its
+  // query heads) share one XCD and its L2
+  const int split = blockIdx.x / NKV, kvh = blockIdx.x % NKV;
+#else
   const int split = blockIdx.x, kvh = blockIdx.y;
+#endif
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = kvh * (NH / NKV) + wave;
   const int seq = *a.pos + 1;
@@ -706,7 +718,10 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const
 // Every load of the head (m, l of each split, both output dims of each
 // split) is issued before the first is used: one memory round trip.
 __global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, const int *pos, float *out) {
-  const int h = blockIdx.x, lane = threadIdx.x;
+  // (VX_ATTN_XCD: block b combines query head (NH / NKV) * (b % NKV) + b / NKV,
+  // on the XCD where its KV head's partials were written)
+  const int h = VX_ATTN_XCD ? (NH / NKV) * ((int)blockIdx.x % NKV) + (int)blockIdx.x / NKV : (int)blockIdx.x;
+  const int lane = threadIdx.x;
   // splits with keys (ATTN_LIVE_COMBINE; the others hold m = -inf, l = 0)
   int live = ATTN_SPLITS;
   if (ATTN_LIVE_COMBINE) {
