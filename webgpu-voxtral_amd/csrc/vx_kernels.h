@@ -642,7 +642,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const
 #if VX_ATTN_XCD
   // 1-D grid, block b = split * NKV + kv head: workgroups are dealt to the
   // 8 XCDs round-robin, so a KV head's splits (and the combine blocks of its
-  // query heads) share one XCD and its L2
+  // query heads) run on one XCD
   const int split = blockIdx.x / NKV, kvh = blockIdx.x % NKV;
 #else
   const int split = blockIdx.x, kvh = blockIdx.y;
