@@ -232,9 +232,6 @@ GemvArgs gargs(const uint16_t *W, const float *x, int xs, float *out, int os, in
 
 }  // namespace
 
-#ifndef VX_PF_ATTN_MFMA
-#define VX_PF_ATTN_MFMA 1  // prompt attention on the matrix cores
-#endif
 
 // FM GEMM launch: `rows` output rows in tiles of FTR, RG tiles per block.
 template <int EPI, int K, int RG, int KS, int P, bool KEEP = false>
@@ -243,61 +240,19 @@ void launch_gemm6(hipStream_t st, const Gemm6Args &a, int rows) {
                      0, st, a.W, a.W2, a.B, a.ssq, a.out, a);
 }
 // Launch shapes of the four FM GEMMs <RG, KS, P>, picked on the whole frame
-// loop.  A build with -DVX_FM_SWEEP selects each from a candidate list by
-// the environment (VX_FM_QKV, VX_FM_O, VX_FM_GATEUP, VX_FM_DOWN = index).
-#ifdef VX_FM_SWEEP
-typedef void (*Gemm6Launch)(hipStream_t, const Gemm6Args &, int);
-static int fm_sweep_pick(const char *name, int n) {
-  const char *v = getenv(name);
-  const int i = v ? atoi(v) : 0;
-  return i < 0 || i >= n ? 0 : i;
-}
-#define FM_PICK(list, name) list[fm_sweep_pick(name, (int)(sizeof(list) / sizeof(list[0])))]
-static const Gemm6Launch kFmQkv[] = {
-    launch_gemm6<EPI_QKV, DIM, 1, 4, 8>,  launch_gemm6<EPI_QKV, DIM, 1, 8, 6>,
-    launch_gemm6<EPI_QKV, DIM, 1, 8, 12>, launch_gemm6<EPI_QKV, DIM, 1, 8, 4>,
-    launch_gemm6<EPI_QKV, DIM, 1, 4, 12>, launch_gemm6<EPI_QKV, DIM, 1, 6, 8>,
-    launch_gemm6<EPI_QKV, DIM, 1, 12, 8>, launch_gemm6<EPI_QKV, DIM, 1, 16, 6>,
-    launch_gemm6<EPI_QKV, DIM, 2, 4, 6>,  launch_gemm6<EPI_QKV, DIM, 2, 8, 4>};
-static const Gemm6Launch kFmO[] = {
-    launch_gemm6<EPI_RESID, QD, 1, 8, 16>, launch_gemm6<EPI_RESID, QD, 1, 16, 8>,
-    launch_gemm6<EPI_RESID, QD, 1, 8, 8>,  launch_gemm6<EPI_RESID, QD, 1, 16, 4>,
-    launch_gemm6<EPI_RESID, QD, 2, 8, 8>,  launch_gemm6<EPI_RESID, QD, 1, 4, 16>,
-    launch_gemm6<EPI_RESID, QD, 1, 16, 2>, launch_gemm6<EPI_RESID, QD, 2, 4, 16>};
-static const Gemm6Launch kFmGateUp[] = {
-    launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 16>, launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 12>,
-    launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 8>,  launch_gemm6<EPI_SWIGLU, DIM, 1, 2, 16>,
-    launch_gemm6<EPI_SWIGLU, DIM, 1, 4, 8>,  launch_gemm6<EPI_SWIGLU, DIM, 1, 4, 12>,
-    launch_gemm6<EPI_SWIGLU, DIM, 1, 8, 12>, launch_gemm6<EPI_SWIGLU, DIM, 1, 8, 6>,
-    launch_gemm6<EPI_SWIGLU, DIM, 2, 1, 16>};
-static const Gemm6Launch kFmDown[] = {
-    launch_gemm6<EPI_RESID, HID, 1, 12, 12>, launch_gemm6<EPI_RESID, HID, 1, 12, 24>,
-    launch_gemm6<EPI_RESID, HID, 1, 12, 8>,  launch_gemm6<EPI_RESID, HID, 1, 8, 12>,
-    launch_gemm6<EPI_RESID, HID, 1, 16, 9>,  launch_gemm6<EPI_RESID, HID, 1, 16, 18>,
-    launch_gemm6<EPI_RESID, HID, 1, 6, 16>,  launch_gemm6<EPI_RESID, HID, 1, 6, 24>,
-    launch_gemm6<EPI_RESID, HID, 1, 9, 16>,  launch_gemm6<EPI_RESID, HID, 1, 4, 24>};
-static const Gemm6Launch kFmO0[] = {launch_gemm6<EPI_RESID, QD, 1, 8, 16, true>,
-                                     launch_gemm6<EPI_RESID, QD, 1, 16, 4, true>};
-#define FM_GEMM_QKV FM_PICK(kFmQkv, "VX_FM_QKV")
-#define FM_GEMM_O FM_PICK(kFmO, "VX_FM_O")
-#define FM_GEMM_O_KEEP FM_PICK(kFmO0, "VX_FM_O0")
-#define FM_GEMM_GATEUP FM_PICK(kFmGateUp, "VX_FM_GATEUP")
-#define FM_GEMM_DOWN FM_PICK(kFmDown, "VX_FM_DOWN")
-#else
+// loop.
 #define FM_GEMM_QKV (launch_gemm6<EPI_QKV, DIM, 1, 4, 8>)
 #define FM_GEMM_O (launch_gemm6<EPI_RESID, QD, 1, 8, 16>)
 #define FM_GEMM_O_KEEP (launch_gemm6<EPI_RESID, QD, 1, 8, 16, true>)
 #define FM_GEMM_GATEUP (launch_gemm6<EPI_SWIGLU, DIM, 1, 1, 16>)
 #define FM_GEMM_DOWN (launch_gemm6<EPI_RESID, HID, 1, 12, 12>)
-#endif
 // 12-row tiles divide every FM matrix into a multiple of 256 tiles
 static_assert(QKV_ROWS % (256 * FTR) == 0 && DIM % (256 * FTR) == 0 && HID % (256 * FTR) == 0 &&
                   DIM / FTR <= SSQ_MAX && DIM % 256 == 0,
               "FM GEMM tiles");
 
-// decode attention partials: (splits, KV heads), or one dimension when a KV
-// head's blocks are grouped on one XCD
-static dim3 attn_grid() { return VX_ATTN_XCD ? dim3(ATTN_SPLITS * NKV) : dim3(ATTN_SPLITS, NKV); }
+// decode attention partials: one block per (split, KV head)
+static dim3 attn_grid() { return dim3(ATTN_SPLITS * NKV); }
 
 // Streaming GEMV launch: M units split exactly into blocks of WAVES*UPW.
 template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K, int D = 2>
@@ -306,39 +261,12 @@ void launch_gemv1(hipStream_t st, const GemvArgs &a) {
   hipLaunchKernelGGL((gemv1_kernel<WAVES, UPW, UPG, EPI, NORM, K, D>), dim3(a.M / per_block),
                      dim3(WAVES * 64), 0, st, a.W, a.W2, a.x, a.norm_w, a.out, a);
 }
-// Backbone GEMV launch shapes (waves per block, one unit per wave).  A build
-// with -DVX_BB_SWEEP selects each from a candidate list by the environment
-// (VX_BB_QKV, VX_BB_O, VX_BB_GATEUP, VX_BB_DOWN = index).
-#ifdef VX_BB_SWEEP
-typedef void (*GemvLaunch)(hipStream_t, const GemvArgs &);
-static int bb_sweep_pick(const char *name, int n) {
-  const char *v = getenv(name);
-  const int i = v ? atoi(v) : 0;
-  return i < 0 || i >= n ? 0 : i;
-}
-#define BB_PICK(list, name) list[bb_sweep_pick(name, (int)(sizeof(list) / sizeof(list[0])))]
-static const GemvLaunch kBbQkv[] = {
-    launch_gemv1<6, 1, 1, EPI_QKV_ROPE, true, DIM, 1>, launch_gemv1<4, 1, 1, EPI_QKV_ROPE, true, DIM, 1>,
-    launch_gemv1<8, 1, 1, EPI_QKV_ROPE, true, DIM, 1>, launch_gemv1<12, 1, 1, EPI_QKV_ROPE, true, DIM, 1>};
-static const GemvLaunch kBbO[] = {
-    launch_gemv1<12, 1, 1, EPI_RESID, false, QD, 1>, launch_gemv1<6, 1, 1, EPI_RESID, false, QD, 1>,
-    launch_gemv1<8, 1, 1, EPI_RESID, false, QD, 1>, launch_gemv1<4, 1, 1, EPI_RESID, false, QD, 1>};
-static const GemvLaunch kBbGateUp[] = {
-    launch_gemv1<12, 1, 1, EPI_SWIGLU, true, DIM, 1>, launch_gemv1<8, 1, 1, EPI_SWIGLU, true, DIM, 1>,
-    launch_gemv1<16, 1, 1, EPI_SWIGLU, true, DIM, 1>};
-static const GemvLaunch kBbDown[] = {
-    launch_gemv1<6, 1, 1, EPI_RESID, false, HID, 1>, launch_gemv1<4, 1, 1, EPI_RESID, false, HID, 1>,
-    launch_gemv1<8, 1, 1, EPI_RESID, false, HID, 1>, launch_gemv1<12, 1, 1, EPI_RESID, false, HID, 1>};
-#define BB_GEMV_QKV BB_PICK(kBbQkv, "VX_BB_QKV")
-#define BB_GEMV_O BB_PICK(kBbO, "VX_BB_O")
-#define BB_GEMV_GATEUP BB_PICK(kBbGateUp, "VX_BB_GATEUP")
-#define BB_GEMV_DOWN BB_PICK(kBbDown, "VX_BB_DOWN")
-#else
+// Backbone GEMV launch shapes (waves per block, one unit per wave), picked
+// by a sweep over 4-16 waves per block on the decode step.
 #define BB_GEMV_QKV (launch_gemv1<6, 1, 1, EPI_QKV_ROPE, true, DIM, 1>)
 #define BB_GEMV_O (launch_gemv1<12, 1, 1, EPI_RESID, false, QD, 1>)
 #define BB_GEMV_GATEUP (launch_gemv1<12, 1, 1, EPI_SWIGLU, true, DIM, 1>)
 #define BB_GEMV_DOWN (launch_gemv1<6, 1, 1, EPI_RESID, false, HID, 1>)
-#endif
 // unit counts of the backbone GEMVs must split into whole blocks
 static_assert((QKV_ROWS / 2) % 6 == 0 && DIM % 12 == 0 && HID % 12 == 0 && DIM % 6 == 0,
               "launch shapes");
@@ -369,7 +297,7 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
     else
       hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, attn_grid(), dim3(256), 0, st, a.pos, a.kc,
                          a.vc, a.q, a);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->pos, e->attn);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->attn);
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
     GemvArgs a = gargs(W.wo, e->attn, QD, e->x, 0, DIM);
@@ -1638,20 +1566,14 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
       hipLaunchKernelGGL(pf_qkv_epi_kernel<NS>, dim3(n, QKV_ROWS / 2 / 256), blk, 0, st, e->pf_c, nt,
                          e->pf_q, e->kc(l), e->vc(l), e->kv_f32, e->max_seq, pos0, e->inv_freq);
     });
-    if (e->kv_f32 && VX_PF_ATTN_MFMA)
+    if (e->kv_f32)
       hipLaunchKernelGGL(pf_attn_mfma_kernel<float>, dim3(nt / PFA_T, NKV), dim3(256 * PFA_KG), PFA_LDS,
                          st, e->pf_q, (const float *)e->kc(l), (const float *)e->vc(l), e->max_seq, pos0,
                          n, nt, e->pf_b);
-    else if (VX_PF_ATTN_MFMA)
+    else
       hipLaunchKernelGGL(pf_attn_mfma_kernel<uint16_t>, dim3(nt / PFA_T, NKV), dim3(256 * PFA_KG),
                          PFA_LDS, st, e->pf_q, (const uint16_t *)e->kc(l), (const uint16_t *)e->vc(l),
                          e->max_seq, pos0, n, nt, e->pf_b);
-    else if (e->kv_f32)
-      hipLaunchKernelGGL(pf_attn_kernel<float>, dim3(nt, NKV), blk, 0, st, e->pf_q, e->kc(l),
-                         e->vc(l), e->max_seq, pos0, n, nt, e->pf_b);
-    else
-      hipLaunchKernelGGL(pf_attn_kernel<uint16_t>, dim3(nt, NKV), blk, 0, st, e->pf_q, e->kc(l),
-                         e->vc(l), e->max_seq, pos0, n, nt, e->pf_b);
     if ((rc = pf_gemm(e, W.wo, DIM, QD, nt, &ns))) return rc;
     gm_with_slices(ns, [&](auto NS) {
       hipLaunchKernelGGL((pf_resid_pack_kernel<true, NS>), dim3(nt), blk, 0, st, e->pf_c, n, nt, e->pf_x,

@@ -36,28 +36,9 @@ constexpr int HID = 9216;
 constexpr int QKV_ROWS = QD + 2 * KVD;  // 6144
 constexpr int NAC = 36;
 constexpr int SEMV = 8320;
-// Decode attention split over the key axis: ATTN_SPLITS blocks per KV head.
-// With ATTN_TILE_ALIGN a split takes whole tiles of 32 keys (so at short
-// context some splits have no keys), and with ATTN_LIVE_COMBINE the combine
-// reads only the splits that have keys.
-#ifndef VX_ATTN_SPLITS
-#define VX_ATTN_SPLITS 32
-#endif
-#ifndef VX_ATTN_TILE_ALIGN
-#define VX_ATTN_TILE_ALIGN 0
-#endif
-#ifndef VX_ATTN_LIVE_COMBINE
-#define VX_ATTN_LIVE_COMBINE 0
-#endif
-// one KV head's attention blocks on one XCD (see attn_partial_kernel); 0
-// keeps the 2-D (split, KV head) grid
-#ifndef VX_ATTN_XCD
-#define VX_ATTN_XCD 1
-#endif
-constexpr int ATTN_SPLITS = VX_ATTN_SPLITS;
-constexpr bool ATTN_TILE_ALIGN = VX_ATTN_TILE_ALIGN != 0;
-constexpr bool ATTN_LIVE_COMBINE = VX_ATTN_LIVE_COMBINE != 0;
-static_assert(ATTN_SPLITS <= 64 && (ATTN_SPLITS & (ATTN_SPLITS - 1)) == 0, "splits: power of 2, <= 64");
+// Decode attention is split over the key axis: ATTN_SPLITS blocks per KV
+// head, each taking ceil(keys / ATTN_SPLITS) keys.
+constexpr int ATTN_SPLITS = 32;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -67,16 +48,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 // loads carry the non-temporal hint (global_load_dwordx4 ... nt): on MI355X
 // these stream faster than plain loads and neither allocate in nor evict
 // from the memory-side Infinity Cache.
-#ifndef VX_WEIGHT_NT
-#define VX_WEIGHT_NT 1
-#endif
-__device__ __forceinline__ u32x4 ldw(const void *p) {
-#if VX_WEIGHT_NT
-  return __builtin_nontemporal_load((const u32x4 *)p);
-#else
-  return *(const u32x4 *)p;
-#endif
-}
+__device__ __forceinline__ u32x4 ldw(const void *p) { return __builtin_nontemporal_load((const u32x4 *)p); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -568,15 +540,8 @@ struct AttnArgs {
 
 constexpr int AT_T = 32;  // keys per LDS tile
 
-// keys per split for seq keys: ceil(seq / ATTN_SPLITS), or (ATTN_TILE_ALIGN)
-// that many rounded up to whole tiles
-__device__ __forceinline__ int attn_chunk(int seq) {
-  if (ATTN_TILE_ALIGN) {
-    const int tiles = (seq + AT_T - 1) / AT_T;
-    return (tiles + ATTN_SPLITS - 1) / ATTN_SPLITS * AT_T;
-  }
-  return (seq + ATTN_SPLITS - 1) / ATTN_SPLITS;
-}
+// keys per split for seq keys
+__device__ __forceinline__ int attn_chunk(int seq) { return (seq + ATTN_SPLITS - 1) / ATTN_SPLITS; }
 
 // Geometry of one K or V tile of AT_T rows staged through LDS: 16-byte
 // chunks, CPT per thread (256 threads), rows padded by 16 bytes so that the
@@ -621,13 +586,16 @@ __device__ __forceinline__ float2 vpair(const uint16_t *v) {
 }
 
 // Partials (attnScore + softmax + attnValue, src/shaders.ts:306-447, split
-// over the key axis): grid (ATTN_SPLITS, NKV), 256 threads, wave w = query
-// head 4*kv_head + w, so the four heads sharing a KV head share every staged
-// tile.  Split s covers keys [s*chunk, min(seq, (s+1)*chunk)), chunk =
-// ceil(seq / ATTN_SPLITS).  Per tile of AT_T keys: lane l scores key l%32
-// over dims [(l/32)*64, +64) (halves joined by one shuffle), an online
-// softmax update, then lane l accumulates P.V for dims 2l, 2l+1.  The next
-// tile's loads are in flight while the current one is computed.
+// over the key axis): 1-D grid of ATTN_SPLITS * NKV blocks of 256 threads,
+// block b = split * NKV + kv head.  Workgroups are dealt to the 8 XCDs
+// round-robin, so a KV head's splits (and the combine blocks of its query
+// heads) run on one XCD.  Wave w is query head 4*kv_head + w, so the four
+// heads sharing a KV head share every staged tile.  Split s covers keys
+// [s*chunk, min(seq, (s+1)*chunk)), chunk = ceil(seq / ATTN_SPLITS).
+// Per tile of AT_T keys: lane l scores key l%32 over dims [(l/32)*64, +64)
+// (halves joined by one shuffle), an online softmax update, then lane l
+// accumulates P.V for dims 2l, 2l+1.  The next tile's loads are in flight
+// while the current one is computed.
 template <typename KVT>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const void *kc, const void *vc,
                                                            const float *q, AttnArgs args) {
@@ -639,14 +607,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const
   a.vc = vc;
   a.q = q;
   using G = KvTile<KVT>;
-#if VX_ATTN_XCD
-  // 1-D grid, block b = split * NKV + kv head: workgroups are dealt to the
-  // 8 XCDs round-robin, so a KV head's splits (and the combine blocks of its
-  // query heads) run on one XCD
   const int split = blockIdx.x / NKV, kvh = blockIdx.x % NKV;
-#else
-  const int split = blockIdx.x, kvh = blockIdx.y;
-#endif
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = kvh * (NH / NKV) + wave;
   const int seq = *a.pos + 1;
@@ -713,35 +674,28 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const
   }
 }
 
-// Combine: one wave per query head.  M = max m_s, L = sum l_s e^(m_s - M),
-// o = sum o_s e^(m_s - M) / L (splits without keys carry m = -inf, l = 0).
-// Every load of the head (m, l of each split, both output dims of each
-// split) is issued before the first is used: one memory round trip.
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, const int *pos, float *out) {
-  // (VX_ATTN_XCD: block b combines query head (NH / NKV) * (b % NKV) + b / NKV,
-  // on the XCD where its KV head's partials were written)
-  const int h = VX_ATTN_XCD ? (NH / NKV) * ((int)blockIdx.x % NKV) + (int)blockIdx.x / NKV : (int)blockIdx.x;
+// Combine: one wave per query head; block b combines query head
+// (NH / NKV) * (b % NKV) + b / NKV, on the XCD where its KV head's partials
+// were written.  M = max m_s, L = sum l_s e^(m_s - M), o = sum o_s e^(m_s -
+// M) / L (splits without keys carry m = -inf, l = 0).  Every load of the head
+// (m, l of each split, both output dims of each split) is issued before the
+// first is used: one memory round trip.
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, float *out) {
+  const int h = (NH / NKV) * ((int)blockIdx.x % NKV) + (int)blockIdx.x / NKV;
   const int lane = threadIdx.x;
-  // splits with keys (ATTN_LIVE_COMBINE; the others hold m = -inf, l = 0)
-  int live = ATTN_SPLITS;
-  if (ATTN_LIVE_COMBINE) {
-    const int seq = *pos + 1, chunk = attn_chunk(seq);
-    live = (seq + chunk - 1) / chunk;
-  }
+  static_assert(ATTN_SPLITS <= 64, "one lane per split");
   const float *hp = part + (size_t)h * ATTN_SPLITS * (HD + 2);
   const float *mlp = hp + (lane & (ATTN_SPLITS - 1)) * (HD + 2) + HD;
-  const bool lane_live = lane < ATTN_SPLITS && lane < live;
+  const bool lane_live = lane < ATTN_SPLITS;
   const float mv = lane_live ? mlp[0] : -INFINITY, lv = lane_live ? mlp[1] : 0.f;
   float2 o[ATTN_SPLITS];
 #pragma unroll
-  for (int s = 0; s < ATTN_SPLITS; s++)
-    o[s] = s < live ? *(const float2 *)(hp + s * (HD + 2) + lane * 2) : make_float2(0.f, 0.f);
+  for (int s = 0; s < ATTN_SPLITS; s++) o[s] = *(const float2 *)(hp + s * (HD + 2) + lane * 2);
   // keep every load ahead of the first use (one memory round trip)
   __builtin_amdgcn_sched_barrier(0);
-  const float ms = lane < ATTN_SPLITS ? mv : -INFINITY;
-  const float M = wave_max(ms);
-  const float wgt = lane < ATTN_SPLITS ? expf(ms - M) : 0.f;
-  const float L = wave_sum(lane < ATTN_SPLITS ? lv * wgt : 0.f);
+  const float M = wave_max(mv);
+  const float wgt = lane_live ? expf(mv - M) : 0.f;
+  const float L = wave_sum(lane_live ? lv * wgt : 0.f);
   float r0 = 0.f, r1 = 0.f;
 #pragma unroll
   for (int s = 0; s < ATTN_SPLITS; s++) {

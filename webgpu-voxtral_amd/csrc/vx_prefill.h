@@ -202,86 +202,10 @@ __global__ __launch_bounds__(128) void pf_swiglu_pack_kernel(const float *C, int
 }
 static_assert(DIM % 8 == 0 && (HID / 8) % 128 == 0, "prefill packing groups");
 
-// Causal attention of the chunk: query t (position pos0 + t) over keys
-// 0..pos0 + t of the cache.  Grid (nt, NKV), 4 waves = the 4 query heads of
-// the KV head; keys in LDS tiles of AT_T with an online softmax.  The result
-// goes to the O GEMM's B (K = QD) in hi/lo form; blocks of tokens t >= n
-// write zero columns.
-template <typename KVT>
-__global__ __launch_bounds__(256) void pf_attn_kernel(const float *Q, const void *kc, const void *vc,
-                                                      int max_seq, int pos0, int n, int nt, h8 *B) {
-  using G = KvTile<KVT>;
-  const int t = blockIdx.x, kvh = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int h = kvh * (NH / NKV) + wave;
-  _Float16 *bh = (_Float16 *)B + (size_t)t * QD + h * HD + lane * 2;
-  _Float16 *bl = (_Float16 *)B + (size_t)(nt + t) * QD + h * HD + lane * 2;
-  if (t >= n) {
-    *(uint32_t *)bh = 0u;
-    *(uint32_t *)bl = 0u;
-    return;
-  }
-  const int p1 = pos0 + t + 1;
-  __shared__ __attribute__((aligned(16))) float qs[4][HD];
-  __shared__ __attribute__((aligned(16))) KVT ks[AT_T * G::LDW];
-  __shared__ __attribute__((aligned(16))) KVT vs[AT_T * G::LDW];
-  __shared__ float ps[4][AT_T];
-  const float scale = 1.0f / sqrtf((float)HD);
-  const KVT *Kb = (const KVT *)kc + (size_t)kvh * max_seq * HD;
-  const KVT *Vb = (const KVT *)vc + (size_t)kvh * max_seq * HD;
-  u32x4 kr[G::CPT], vr[G::CPT];
-  attn_load_tile<KVT>(Kb, Vb, 0, min(AT_T, p1), tid, kr, vr);
-  qs[wave][lane * 2] = Q[(size_t)t * QD + h * HD + lane * 2];
-  qs[wave][lane * 2 + 1] = Q[(size_t)t * QD + h * HD + lane * 2 + 1];
-  const int key = lane & (AT_T - 1), half = lane >> 5;
-  float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int pb = 0; pb < p1; pb += AT_T) {
-    const int n = min(AT_T, p1 - pb);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < G::CPT; i++) {
-      const int id = tid + 256 * i, row = id / G::CPR, col = id % G::CPR;
-      *(u32x4 *)(ks + row * G::LDW + col * G::EPC) = kr[i];
-      *(u32x4 *)(vs + row * G::LDW + col * G::EPC) = vr[i];
-    }
-    if (pb + AT_T < p1) attn_load_tile<KVT>(Kb, Vb, pb + AT_T, min(AT_T, p1 - pb - AT_T), tid, kr, vr);
-    __syncthreads();
-    float dot = 0.f;
-    const KVT *kp = ks + key * G::LDW + half * (HD / 2);
-    const float *qp = &qs[wave][half * (HD / 2)];
-#pragma unroll
-    for (int c = 0; c < HD / 2; c += G::EPC) dot = kdot(kp + c, qp + c, dot);
-    dot += __shfl_xor(dot, 32, 64);
-    const bool valid = key < n;
-    const float s = valid ? dot * scale : -INFINITY;
-    const float mnew = fmaxf(m, wave_max(s));
-    const float e = valid ? expf(s - mnew) : 0.f;
-    const float corr = expf(m - mnew);
-    l = l * corr + wave_sum(half ? 0.f : e);
-    o0 *= corr;
-    o1 *= corr;
-    m = mnew;
-    if (!half) ps[wave][key] = e;
-    __syncthreads();
-#pragma unroll 8
-    for (int j = 0; j < AT_T; j++) {
-      const float ej = ps[wave][j];
-      const float2 v = vpair(vs + j * G::LDW + lane * 2);
-      o0 = fmaf(ej, v.x, o0);
-      o1 = fmaf(ej, v.y, o1);
-    }
-  }
-  const float y0 = o0 / l, y1 = o1 / l;
-  h2 hi, lo;
-  split2(y0, y1, hi, lo);
-  *(h2 *)bh = hi;
-  *(h2 *)bl = lo;
-}
-
 // ------------------------------------------------ causal attention on MFMA
-// The same result as pf_attn_kernel<float> (attnScore + softmax + attnValue
-// per prompt token over keys 0..pos0+t, src/shaders.ts:306-447) up to the
-// order of the softmax sums, with the products on the matrix cores.
+// Causal attention of the chunk (attnScore + softmax + attnValue per prompt
+// token over keys 0..pos0+t, src/shaders.ts:306-447) with the products on the
+// matrix cores; blocks of tokens t >= n write zero columns of the O GEMM's B.
 // Block = (16-token tile, KV head) of PFA_KG groups of 4 waves; wave w of a
 // group is query head 4*kv_head + w.  The tile's keys are taken 32 at a
 // time: group g stages tiles g, g + PFA_KG, ... in its own LDS area, K rows
@@ -305,10 +229,7 @@ constexpr int PFA_T = 16;          // tokens per block
 constexpr int PFA_K = 32;          // keys per staged tile
 constexpr int PFA_KW = HD + 8;     // LDS row of K, halves (272 B)
 constexpr int PFA_VW = PFA_K + 4;  // LDS row of V^T, halves (72 B: 16 rows start on 16 distinct even banks)
-#ifndef VX_PFA_KG
-#define VX_PFA_KG 2
-#endif
-constexpr int PFA_KG = VX_PFA_KG;  // key groups per block
+constexpr int PFA_KG = 2;          // key groups per block
 constexpr int PFA_GROUP = 2 * (PFA_K * PFA_KW + HD * PFA_VW);  // halves of one group's area (hi + lo)
 constexpr int PFA_LDS = PFA_KG * PFA_GROUP * 2;                // dynamic LDS bytes (70 KB)
 constexpr int PFA_RED = 2 + 4 * (HD / 16);                     // merged values per lane: m, l, O^T
