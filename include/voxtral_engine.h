@@ -239,7 +239,13 @@ void vx_generate_options_default(vx_generate_options *o);
  * acoustic_out[max_frames][36] receive the codes; audio_out
  * f32[max_frames * VX_FRAME_SAMPLES] receives codecDecode of the generated
  * frames (TTSResult.audio; 1920 samples per frame).  All three are
- * nullable; audio_out needs an engine created with cfg.codec = 1. */
+ * nullable; audio_out needs an engine created with cfg.codec = 1.
+ * After an EOS the engine holds what the EOS frame left, as after the
+ * reference's loop: the position, the residual stream, normed, the semantic
+ * logits, the codes, the FM noise frame counter and the top-p generator
+ * state.  (The device-sampling modes run one frame ahead and undo it.)  The
+ * FM scratch buffers (fm_hidden, x_history, velocities) are not restored:
+ * they hold the discarded frame's values until the next FM pass. */
 int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens,
                 int32_t audio_start, int32_t audio_count, const float *voice,
                 int32_t max_frames, const vx_generate_options *opt,
@@ -306,8 +312,9 @@ int vx_sample_top_p(vx_engine *e, const float *logits, int32_t n, int32_t valid,
  * staging (logits, parameters, state, code: 37 KB) is a file-scope device
  * array of the library, one per GPU, so n is at most 9216 (larger n returns
  * VX_E_RANGE).  Runs on the null stream of the current device and waits for
- * it.  Calls that overlap on one GPU share the array and race.  Errors are
- * read with vx_last_error(NULL). */
+ * it.  Calls from threads of one process take turns on a per-GPU lock;
+ * calls from different processes that overlap on one GPU share the array
+ * and race.  Errors are read with vx_last_error(NULL). */
 int vx_sample_top_p_noalloc(const float *logits, int32_t n, int32_t valid,
                             double top_p, double temperature, uint64_t *state,
                             uint32_t *code);

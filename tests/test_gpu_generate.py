@@ -21,6 +21,7 @@ import math
 import numpy as np
 import pytest
 
+import oracle as O
 from vxtest import (fsq_margin, gpu_engine, max_rel_err, oracle_engine, tts_prompt,
                     voice_rows)
 
@@ -116,7 +117,9 @@ def test_generate_eos_and_position_rollback():
     """EOS (src/engine.ts:2568-2570) at a chosen frame k, in every sampling
     mode, with and without the speculative frame that generate() enqueues
     ahead; framesGenerated, the codes and the position equal the oracle's
-    serial run, and a later step matches the oracle from that state."""
+    serial run.  The state left behind is the EOS frame's: normed, the
+    device codes and the next FM pass with the device noise (frame counter
+    k + 1) match the oracle, and so does a later backbone step."""
     layers, k, seed = 2, 4, 9
     toks, a0, na = tts_prompt(48, 16, seed=3)
     voice = voice_rows(16)
@@ -134,6 +137,7 @@ def test_generate_eos_and_position_rollback():
         g.load_tensor(SEM_HEAD, W)
         o.set_weight(SEM_HEAD, W)
         n_expect = len(toks) + 1 + k  # prompt, kick, steps of frames 1..k
+        post = {}
         for max_frames in (k + 3, k + 1):  # speculative frame k+1 enqueued, or not
             out = g.generate(toks, a0, na, voice, max_frames, sampling="greedy", seed=seed)
             print(f"[eos] greedy, max_frames {max_frames}: {out['stats']['framesGenerated']} "
@@ -142,12 +146,31 @@ def test_generate_eos_and_position_rollback():
             assert out["semanticCodes"] == base["semanticCodes"][:k]
             assert out["acousticCodes"] == base["acousticCodes"][:k]
             assert g.position == n_expect
+            # the state the EOS frame left, then one FM pass from it with the
+            # device noise
+            normed = g.debug_read("normed", 3072)
+            sem, ac = g.get_codes()
+            fm_codes = g.fm_step_and_read()
+            post[max_frames] = (normed, sem, ac, fm_codes, g.debug_read("x_history", 36))
         r2 = o.generate(toks, a0, na, voice, k + 3, noise_seed=seed,
                         forced_semantic=np.array(out["semanticCodes"], np.uint32),
                         forced_acoustic=np.array(out["acousticCodes"], np.uint32).reshape(k, 36),
                         want_logits=True)
         assert r2["frames"] == k and int(r2["semantic"][k]) == 1
         assert o.position == n_expect
+        # frames 0..k drew noise rows 0..k; the next FM pass draws row k + 1
+        noise = O.gen_gauss_f32(seed, "fm.noise", 36 * (k + 2))[36 * (k + 1):]
+        o.fm_forward(noise, batched=True)
+        safe = fsq_margin(o.buffer("x_t")) * 0.1 >= X_TOL  # margin in x units, as in the frame bars
+        for max_frames, (normed, sem, ac, fm_codes, x0) in post.items():
+            err = max_rel_err(normed, ref["normed"][k])
+            print(f"[eos] max_frames {max_frames}: normed max rel err {err:.2e}, "
+                  f"FM codes equal on {int(np.sum(fm_codes[safe] == o.acoustic_codes[safe]))}/"
+                  f"{int(safe.sum())}", flush=True)
+            assert err < 1e-3
+            assert sem == 1 and list(ac) == list(base["acousticCodes"][k])
+            assert np.array_equal(x0, noise)
+            assert np.array_equal(fm_codes[safe], o.acoustic_codes[safe])
         # the state generate() left behind: one more step from it on both sides
         _, gn = g.backbone_step(token=7)
         o.backbone_step(token=7)

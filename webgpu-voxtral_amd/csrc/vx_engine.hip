@@ -95,6 +95,8 @@ struct vx_engine {
   void *aarena = nullptr;
   float *x = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr, *normed = nullptr,
         *logits = nullptr, *part = nullptr, *layer_stage = nullptr;
+  // the state the previous frame left (multi_codebook_kernel saves it)
+  float *x_prev = nullptr, *normed_prev = nullptr, *logits_prev = nullptr;
   int *pos = nullptr, *frame = nullptr;
   uint32_t *sem_code = nullptr, *codes = nullptr, *argmax_res = nullptr;
   uint64_t *noise_seed = nullptr;
@@ -482,11 +484,10 @@ static void enqueue_fm(vx_engine *e, const float *noise_src, bool greedy_code) {
   hipStream_t st = e->st;
   const float alpha = e->cfg.cfg_alpha;
   const float dt = (float)(1.0 / (double)(e->cfg.nfe - 1));
-  {
-    GemvArgs a = gargs(e->fm_sem, e->normed, DIM, e->sem_logits, 0, SEMV);
-    launch_gemv<1, W4, 2, EPI_PLAIN, false, DIM, DIM>(st, a);
-    GemvArgs b = gargs(e->fm_llm, e->normed, DIM, e->fm_llm_out, 0, DIM);
-    launch_gemv<1, W4, 2, EPI_PLAIN, false, DIM, DIM>(st, b);
+  {  // llm_projection + semantic head: the stacked [3072 + 8320][3072] rows
+     // (fm_llm, fm_sem) into the adjacent fm_llm_out, sem_logits
+    GemvArgs a = gargs(e->fm_llm, e->normed, DIM, e->fm_llm_out, 0, DIM + SEMV);
+    launch_gemv1<8, 1, 1, EPI_PLAIN, false, DIM, 1>(st, a);
   }
   for (int s = 0; s < e->nsteps(); s++) {
     // step 0 also takes the unmasked tree argmax (W.semantic_argmax), or the
@@ -527,15 +528,20 @@ static void fm_topp_body(vx_engine *e) {
   hipLaunchKernelGGL(topp_sample_kernel, dim3(1), dim3(TP_NT), 0, e->st, e->sem_logits, SEMV, 8194,
                      e->tp_params, e->rng_state, e->sem_code, e->frame, e->d_frame);
 }
-static void frame_body(vx_engine *e) {
+// A frame's first kernel embeds the previous frame's codes and saves the
+// state that frame left (FrameSave), for generate()'s EOS rollback.
+static void enqueue_frame_embed(vx_engine *e) {
+  const FrameSave sv{e->x_prev, e->normed_prev, e->logits_prev, e->normed, e->sem_logits};
   hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
-                     e->sem_code, e->codes, e->x);
+                     e->sem_code, e->codes, e->x, sv);
+}
+static void frame_body(vx_engine *e) {
+  enqueue_frame_embed(e);
   enqueue_backbone(e);
   fm_greedy_body(e);
 }
 static void frame_topp_body(vx_engine *e) {
-  hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
-                     e->sem_code, e->codes, e->x);
+  enqueue_frame_embed(e);
   enqueue_backbone(e);
   fm_topp_body(e);
 }
@@ -595,7 +601,7 @@ static int prepare_input(vx_engine *e, int32_t token, int32_t mode, const float 
       break;
     case VX_EMBED_CODES:
       hipLaunchKernelGGL(multi_codebook_kernel, dim3(DIM / 256), dim3(256), 0, e->st, e->audio_emb,
-                         e->sem_code, e->codes, e->x);
+                         e->sem_code, e->codes, e->x, FrameSave{});
       break;
     default:
       return fail(e, VX_E_INVALID, "bad embed mode %d", mode);
@@ -622,12 +628,15 @@ static_assert(NA_PARAMS % 8 == 0 && NA_STATE % 8 == 0, "staging alignment");
 constexpr int NA_MAX_DEVICES = 64;
 std::mutex g_na_mu;
 char *g_na_ptr[NA_MAX_DEVICES] = {};
+// held by a call for its whole use of the device's array (copies in, kernel,
+// copies out, sync): calls from threads of one process take turns
+std::mutex g_na_call_mu[NA_MAX_DEVICES];
 }  // namespace
 static __device__ __align__(256) unsigned char scratch[NA_BYTES];
 
 // the array's address on the current device (looked up on the first call
-// there); nullptr and g_create_error set on failure
-static char *noalloc_scratch() {
+// there) and that device's index; nullptr and g_create_error set on failure
+static char *noalloc_scratch(int *dev_out) {
   int dev = -1;
   hipError_t s = hipGetDevice(&dev);
   if (s != hipSuccess || dev < 0 || dev >= NA_MAX_DEVICES) {
@@ -644,6 +653,7 @@ static char *noalloc_scratch() {
     }
     g_na_ptr[dev] = (char *)p;
   }
+  *dev_out = dev;
   return g_na_ptr[dev];
 }
 
@@ -770,9 +780,11 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   for (auto &W : e->L) place_layer(W);
   for (auto &W : e->FL) place_layer(W);
   place(&e->fm_in, (size_t)DIM * NAC);
-  place(&e->fm_llm, (size_t)DIM * DIM);
   place(&e->fm_time, (size_t)DIM * DIM);
   place(&e->fm_norm, DIM);
+  // llm_projection and the semantic head are adjacent: both read W.normed,
+  // so one GEMV streams the 3072 + 8320 rows (their outputs are adjacent too)
+  place(&e->fm_llm, (size_t)DIM * DIM);
   place(&e->fm_sem, (size_t)SEMV * DIM);
   place(&e->fm_ac, (size_t)NAC * DIM);
   e->codec_on = cfg.codec != 0;
@@ -808,6 +820,10 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
     return fail(nullptr, VX_E_NOMEM, "hipMalloc of %zu weight bytes failed", total);
   }
   for (auto &o : offs) *o.dst = (uint16_t *)((char *)e->warena + o.off);
+  if (e->fm_sem != e->fm_llm + (size_t)DIM * DIM) {  // one GEMV streams both (enqueue_fm)
+    vx_destroy(e);
+    return fail(nullptr, VX_E_STATE, "llm_projection and the semantic head are not adjacent");
+  }
 
   add_slot(e, "mm_audio_embeddings.tok_embeddings.weight", e->tok_emb, {cfg.vocab_size, DIM}, false);
   add_slot(e, "mm_audio_embeddings.audio_codebook_embeddings.embeddings.weight", e->audio_emb,
@@ -993,6 +1009,9 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   aplace((void **)&e->fm_act, 6 * HID * 4);
   aplace((void **)&e->fm_llm_out, DIM * 4);
   aplace((void **)&e->sem_logits, SEMV * 4);
+  aplace((void **)&e->x_prev, DIM * 4);
+  aplace((void **)&e->normed_prev, DIM * 4);
+  aplace((void **)&e->logits_prev, SEMV * 4);
   aplace((void **)&e->tproj, (size_t)ns * DIM * 4);
   aplace((void **)&e->xh, (size_t)(ns + 1) * NAC * 4);
   aplace((void **)&e->vel, (size_t)ns * 2 * NAC * 4);
@@ -1012,6 +1031,10 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
     return fail(nullptr, VX_E_NOMEM, "hipMalloc of activations failed");
   }
   for (auto &o : aoffs) *o.first = (char *)e->aarena + o.second;
+  if (e->sem_logits != e->fm_llm_out + DIM) {  // written by one GEMV (enqueue_fm)
+    vx_destroy(e);
+    return fail(nullptr, VX_E_STATE, "fm_hidden and the semantic logits are not adjacent");
+  }
   (void)hipMemsetAsync(e->aarena, 0, abytes, e->st);
   // rope frequencies, src/shaders.ts:224-256: freq_i = 1 / theta^(2i/128), evaluated once
   // here in f32 (the shader evaluates the same expression per element)
@@ -1726,8 +1749,10 @@ int vx_sample_top_p_noalloc(const float *logits, int32_t n, int32_t valid, doubl
       !(top_p > 0.0) || !(top_p <= 1.0))
     return fail(nullptr, VX_E_INVALID, "top-p: n %d, valid %d, temperature %g, top_p %g out of range",
                 n, valid, temperature, top_p);
-  char *base = noalloc_scratch();
+  int dev = 0;
+  char *base = noalloc_scratch(&dev);
   if (!base) return VX_E_DEVICE;
+  std::lock_guard<std::mutex> call_lock(g_na_call_mu[dev]);
   float *d_logits = (float *)(base + NA_LOGITS);
   double *d_params = (double *)(base + NA_PARAMS);
   uint64_t *d_state = (uint64_t *)(base + NA_STATE);
@@ -1993,6 +2018,30 @@ int vx_codec_decode_debug(vx_engine *e, const uint32_t *semantic, const uint32_t
 // sampleTopP, src/engine.ts:247-289, with a seeded uniform in place of
 // Math.random.  Float32Array intermediates, double accumulators, stable
 // descending sort, as the TypeScript does.
+// splitmix64 increment: the device top-p stream advances by it once per frame
+constexpr uint64_t kTopPGamma = 0x9E3779B97F4A7C15ull;
+
+// Puts back the state frame f left when generate() discards the speculative
+// frame f + 1 after frame f's EOS: the position (frame f + 1's step), the
+// residual stream, normed and the semantic logits (saved by frame f + 1's
+// first kernel), frame f's codes, the FM frame counter (f + 1 frames drew
+// noise) and the top-p generator state rng.  Frame f + 1's K/V row lies past
+// the position and is never read.
+static int undo_frame(vx_engine *e, int f, uint32_t code, const uint32_t *codes, uint64_t rng) {
+  int rc = vx_set_position(e, e->host_pos - 1);
+  if (rc) return rc;
+  HIPCHK(e, hipMemcpyAsync(e->x, e->x_prev, DIM * 4, hipMemcpyDeviceToDevice, e->st));
+  HIPCHK(e, hipMemcpyAsync(e->normed, e->normed_prev, DIM * 4, hipMemcpyDeviceToDevice, e->st));
+  HIPCHK(e, hipMemcpyAsync(e->sem_logits, e->logits_prev, SEMV * 4, hipMemcpyDeviceToDevice, e->st));
+  HIPCHK(e, hipMemcpyAsync(e->sem_code, &code, 4, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipMemcpyAsync(e->codes, codes, NAC * 4, hipMemcpyHostToDevice, e->st));
+  HIPCHK(e, hipMemcpyAsync(e->rng_state, &rng, 8, hipMemcpyHostToDevice, e->st));
+  hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, e->st, e->frame, f + 1);
+  LAUNCHCHK(e);
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  return VX_OK;
+}
+
 int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t audio_start,
                 int32_t audio_count, const float *voice, int32_t max_frames,
                 const vx_generate_options *opt_in, vx_frame_cb on_frame, vx_stage_cb on_stage,
@@ -2122,9 +2171,10 @@ int vx_generate(vx_engine *e, const int32_t *tokens, int32_t n_tokens, int32_t a
       uint32_t codes[NAC];
       memcpy(codes, slot + 1, sizeof codes);
       if (code <= 1 && !opt.ignore_eos) {
-        if (ahead) {  // undo the speculative frame's step
+        if (ahead) {  // undo the speculative frame f + 1
           HIPCHK(e, hipStreamSynchronize(e->st));
-          if ((rc = vx_set_position(e, e->host_pos - 1))) return rc;
+          if ((rc = undo_frame(e, f, code, codes, greedy ? rng : rng + (uint64_t)(f + 1) * kTopPGamma)))
+            return rc;
         }
         break;
       }

@@ -714,12 +714,26 @@ __global__ void embed_row_kernel(const uint16_t *table, int token, float *out) {
   if (i < DIM) out[i] = h2f(table[(size_t)token * DIM + i]);
 }
 
+// The state a frame leaves (residual stream, normed, semantic logits), saved
+// by the next frame's first kernel before it is overwritten; generate()
+// puts it back when that next frame is discarded after an EOS.  Null x_prev:
+// no save.
+struct FrameSave {
+  float *x_prev, *normed_prev, *logits_prev;
+  const float *normed, *logits;
+};
+
 // multiCodebookEmbed: semantic row + 36 acoustic rows 8194 + k*23 + code_k,
 // summed in that order.
 __global__ void multi_codebook_kernel(const uint16_t *table, const uint32_t *sem,
-                                      const uint32_t *codes, float *out) {
+                                      const uint32_t *codes, float *out, FrameSave sv) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= DIM) return;
+  if (sv.x_prev) {
+    sv.x_prev[i] = out[i];
+    sv.normed_prev[i] = sv.normed[i];
+    for (int j = i; j < SEMV; j += DIM) sv.logits_prev[j] = sv.logits[j];
+  }
   // all 37 row indices, then all 37 row elements, then the ordered sum
   uint32_t row[NAC + 1];
   row[0] = sem[0];

@@ -827,6 +827,8 @@ napi_value generate(napi_env env, napi_callback_info info) {
   napi_create_string_utf8(env, "voxtral.generate", NAPI_AUTO_LENGTH, &name);
   if (napi_create_threadsafe_function(env, nullptr, nullptr, name, 0, 1, nullptr, nullptr, j,
                                       dispatch, &j->events) != napi_ok) {
+    if (j->on_frame) napi_delete_reference(env, j->on_frame);
+    if (j->on_stage) napi_delete_reference(env, j->on_stage);
     delete j;
     napi_throw_error(env, nullptr, "could not create the generate event queue");
     return nullptr;
