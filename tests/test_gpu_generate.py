@@ -71,8 +71,12 @@ def forced_oracle(o, toks, a0, na, voice, gpu, max_frames, seed, ignore_eos=Fals
                       want_logits=True, **kw)
 
 
-@pytest.mark.parametrize("layers,n_tok,n_voice,frames", [(2, 256, 64, 12), (26, 64, 32, 8)])
+@pytest.mark.parametrize("layers,n_tok,n_voice,frames", [(2, 256, 64, 12), (26, 64, 32, 100)])
 def test_generate_matches_oracle(layers, n_tok, n_voice, frames):
+    """generate() in greedy mode, through the captured frame graphs the
+    benchmark times, frame by frame against the oracle's serial run
+    (src/engine.ts:2498-2585); at full depth over 100 frames, so that the
+    bar of identical codes on >= 99% of frames is a count of 99."""
     print(f"[generate] {layers} layers, {n_tok}-token prompt, {n_voice} voice rows, "
           f"{frames} frames", flush=True)
     toks, a0, na = tts_prompt(n_tok, n_voice, seed=layers)
