@@ -363,6 +363,18 @@ int vx_time_frames(vx_engine *e, int32_t n, float *ms);
 int vx_time_kernel(vx_engine *e, int32_t kernel, int32_t iters, float *avg_us,
                    double *bytes);
 
+/* Launch timeline of one decode step (no counterpart in the reference: a
+ * measurement without a profiler).  Replays a copy of the held decode step's
+ * graph reps times (the same kernels as VX_TIME_HOLD) in which every block
+ * of every launch folds its start and end time on the GPU's 100 MHz wall
+ * clock into its launch's slot.  stamps[2 i], stamps[2 i + 1] receive the
+ * earliest block start and the latest block end of launch i of the last
+ * replay: i = 6 l + k for layer l (k: 0 QKV, 1 attention partials,
+ * 2 combine, 3 O, 4 gate/up, 5 down), then the final norm;
+ * *n_out = 6 * n_layers + 1 launches, cap >= 2 * *n_out. */
+int vx_debug_timeline(vx_engine *e, int32_t reps, uint64_t *stamps, int32_t cap,
+                      int32_t *n_out);
+
 int vx_synchronize(vx_engine *e);
 
 #ifdef __cplusplus

@@ -290,6 +290,36 @@ def test_full_backbone_decode_at_512(pair26):
     assert max_rel_err(g.debug_read("hidden", 3072), o.buffer("hidden")) < 1e-2
 
 
+def test_decode_at_512_after_real_prefill(pair26):
+    """The headline workload as the benchmark builds it: a 512-token prefix of
+    ids drawn uniformly from the 131072-token vocabulary (seed 0) prefilled
+    with the batched GEMM prefill, then a decode step at position 512 (513
+    keys) through all 26 layers.  The oracle runs the reference's per-token
+    prefill (src/engine.ts:2457-2472) and the same step.  Checked: normed,
+    the residual stream, and the K/V rows of layers 0, 12 and 25."""
+    g, o = pair26
+    g.reset()
+    o.reset()
+    toks = np.random.default_rng(0).integers(0, 131072, 512)
+    g.prefill(toks)
+    for t in toks:
+        o.backbone_step(int(t))
+    assert g.position == o.position == 512
+    x = O.gen_f32(SEED, "input.hidden", 3072)
+    _, gn = g.backbone_step(precomputed=x)
+    o.backbone_step(precomputed=x)
+    err = max_rel_err(gn, o.buffer("normed"))
+    herr = max_rel_err(g.debug_read("hidden", 3072), o.buffer("hidden"))
+    print(f"[c1] decode at 512 after a real prefill: normed {err:.2e}, hidden {herr:.2e}", flush=True)
+    assert err < 1e-2 and ref_allclose(gn, o.buffer("normed"))
+    assert herr < 1e-2
+    for l in (0, 12, 25):
+        for w in (0, 1):
+            kerr = max_rel_err(g.read_kv(l, w, 0, 513), o.kv(l, w)[:513])
+            print(f"[c1] layer {l} {'KV'[w]} rows 0..512: {kerr:.2e}", flush=True)
+            assert kerr < 1e-2, (l, w, kerr)
+
+
 def test_full_backbone_real_prefill(pair26):
     """Prompt tokens through all 26 layers from position 0 (real KV)."""
     g, o = pair26

@@ -97,6 +97,8 @@ struct vx_engine {
         *logits = nullptr, *part = nullptr, *layer_stage = nullptr;
   // the state the previous frame left (multi_codebook_kernel saves it)
   float *x_prev = nullptr, *normed_prev = nullptr, *logits_prev = nullptr;
+  // launch timeline of one step: [6 * n_layers + 1][TS_BLOCKS][start, end] wall-clock stamps
+  unsigned long long *timeline = nullptr;
   int *pos = nullptr, *frame = nullptr;
   uint32_t *sem_code = nullptr, *codes = nullptr, *argmax_res = nullptr;
   uint64_t *noise_seed = nullptr;
@@ -125,7 +127,7 @@ struct vx_engine {
 
   int host_pos = 0;
   hipGraphExec_t step_exec = nullptr, hold_exec = nullptr, feedback_exec = nullptr,
-                 frame_exec = nullptr,
+                 frame_exec = nullptr, timeline_exec = nullptr,
                  fm_greedy_exec = nullptr, fm_plain_exec = nullptr;
   bool use_graphs = true;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -261,7 +263,7 @@ template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K, int D = 2>
 void launch_gemv1(hipStream_t st, const GemvArgs &a) {
   constexpr int per_block = WAVES * UPW;
   hipLaunchKernelGGL((gemv1_kernel<WAVES, UPW, UPG, EPI, NORM, K, D>), dim3(a.M / per_block),
-                     dim3(WAVES * 64), 0, st, a.W, a.W2, a.x, a.norm_w, a.out, a);
+                     dim3(WAVES * 64), 0, st, a.W, a.W2, a.x, a.norm_w, a.out, a.ts, a);
 }
 // Backbone GEMV launch shapes (waves per block, one unit per wave), picked
 // by a sweep over 4-16 waves per block on the decode step.
@@ -276,9 +278,13 @@ static_assert((QKV_ROWS / 2) % 6 == 0 && DIM % 12 == 0 && HID % 12 == 0 && DIM %
 // One backbone layer: 6 launches (norm + QKV + rope + KV write | attention
 // partials | attention combine | O + residual | norm + gate/up + SwiGLU |
 // down + residual).
-static void enqueue_layer(vx_engine *e, int l, int only = -1) {
+// ts: the step's launch timeline (vx_debug_timeline), or null; launch k of
+// layer l (0 QKV, 1 attention partials, 2 combine, 3 O, 4 gate/up, 5 down)
+// writes its blocks' stamps to slot 6 l + k (2 * TS_BLOCKS values).
+static void enqueue_layer(vx_engine *e, int l, int only = -1, unsigned long long *ts = nullptr) {
   const LayerW &W = e->L[l];
   hipStream_t st = e->st;
+  auto slot = [&](int k) { return ts ? ts + (size_t)2 * TS_BLOCKS * (6 * l + k) : nullptr; };
   if (only < 0 || only == VX_KERNEL_QKV) {
     GemvArgs a = gargs(W.wqkv, e->x, DIM, e->q, 0, QKV_ROWS / 2);
     a.norm_w = W.attn_norm;
@@ -289,20 +295,22 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
     a.kv_f32 = e->kv_f32;
     a.max_seq = e->max_seq;
     a.inv_freq = e->inv_freq;
+    a.ts = slot(0);
     BB_GEMV_QKV(st, a);
   }
   if (only < 0 || only == VX_KERNEL_ATTN) {
-    AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn};
+    AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn, slot(1)};
     if (e->kv_f32)
       hipLaunchKernelGGL(attn_partial_kernel<float>, attn_grid(), dim3(256), 0, st, a.pos, a.kc,
-                         a.vc, a.q, a);
+                         a.vc, a.q, a.ts, a);
     else
       hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, attn_grid(), dim3(256), 0, st, a.pos, a.kc,
-                         a.vc, a.q, a);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->attn);
+                         a.vc, a.q, a.ts, a);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->attn, slot(2));
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
     GemvArgs a = gargs(W.wo, e->attn, QD, e->x, 0, DIM);
+    a.ts = slot(3);
     BB_GEMV_O(st, a);
   }
   if (only < 0 || only == VX_KERNEL_GATEUP) {
@@ -310,21 +318,26 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1) {
     a.W2 = W.w3;
     a.norm_w = W.ffn_norm;
     a.eps = e->cfg.norm_eps;
+    a.ts = slot(4);
     BB_GEMV_GATEUP(st, a);
   }
   if (only < 0 || only == VX_KERNEL_DOWN) {
     GemvArgs a = gargs(W.w2, e->act, HID, e->x, 0, DIM);
+    a.ts = slot(5);
     BB_GEMV_DOWN(st, a);
   }
 }
 
-static void enqueue_backbone_at(vx_engine *e, bool advance) {
-  for (int l = 0; l < e->cfg.n_layers; l++) enqueue_layer(e, l);
+static void enqueue_backbone_at(vx_engine *e, bool advance, unsigned long long *ts = nullptr) {
+  for (int l = 0; l < e->cfg.n_layers; l++) enqueue_layer(e, l, -1, ts);
   hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->final_norm,
-                     e->cfg.norm_eps, e->normed, advance ? e->pos : nullptr);
+                     e->cfg.norm_eps, e->normed, advance ? e->pos : nullptr,
+                     ts ? ts + (size_t)2 * TS_BLOCKS * 6 * e->cfg.n_layers : nullptr);
 }
 static void enqueue_backbone(vx_engine *e) { enqueue_backbone_at(e, true); }
 static void enqueue_backbone_hold(vx_engine *e) { enqueue_backbone_at(e, false); }
+// the held step with its launch timeline recorded (vx_debug_timeline)
+static void enqueue_backbone_timeline(vx_engine *e) { enqueue_backbone_at(e, false, e->timeline); }
 
 __global__ void copy_dim_kernel(const float *src, float *dst) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1009,6 +1022,7 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   aplace((void **)&e->fm_act, 6 * HID * 4);
   aplace((void **)&e->fm_llm_out, DIM * 4);
   aplace((void **)&e->sem_logits, SEMV * 4);
+  aplace((void **)&e->timeline, (size_t)(6 * cfg.n_layers + 1) * TS_BLOCKS * 16);
   aplace((void **)&e->x_prev, DIM * 4);
   aplace((void **)&e->normed_prev, DIM * 4);
   aplace((void **)&e->logits_prev, SEMV * 4);
@@ -1056,6 +1070,7 @@ void vx_destroy(vx_engine *e) {
   if (e->st) (void)hipStreamSynchronize(e->st);
   if (e->step_exec) (void)hipGraphExecDestroy(e->step_exec);
   if (e->hold_exec) (void)hipGraphExecDestroy(e->hold_exec);
+  if (e->timeline_exec) (void)hipGraphExecDestroy(e->timeline_exec);
   if (e->feedback_exec) (void)hipGraphExecDestroy(e->feedback_exec);
   if (e->fm_greedy_exec) (void)hipGraphExecDestroy(e->fm_greedy_exec);
   if (e->fm_topp_exec) (void)hipGraphExecDestroy(e->fm_topp_exec);
@@ -1288,19 +1303,19 @@ static int debug_layers_step(vx_engine *e, int32_t token, int32_t mode, const fl
   for (int l = 0; l < e->cfg.n_layers; l++) {
     const int r = 1 + 4 * l;
     hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->L[l].attn_norm, eps,
-                       stage(r), nullptr);
+                       stage(r), nullptr, nullptr);
     enqueue_layer(e, l, VX_KERNEL_QKV);
     enqueue_layer(e, l, VX_KERNEL_ATTN);
     enqueue_layer(e, l, VX_KERNEL_OPROJ);
     HIPCHK(e, hipMemcpyAsync(stage(r + 1), e->x, DIM * 4, hipMemcpyDeviceToDevice, e->st));
     hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->L[l].ffn_norm, eps,
-                       stage(r + 2), nullptr);
+                       stage(r + 2), nullptr, nullptr);
     enqueue_layer(e, l, VX_KERNEL_GATEUP);
     enqueue_layer(e, l, VX_KERNEL_DOWN);
     HIPCHK(e, hipMemcpyAsync(stage(r + 3), e->x, DIM * 4, hipMemcpyDeviceToDevice, e->st));
   }
   hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, e->st, e->x, e->final_norm, eps, e->normed,
-                     e->pos);
+                     e->pos, nullptr);
   LAUNCHCHK(e);
   e->host_pos++;
   return VX_OK;
@@ -1620,7 +1635,7 @@ static int enqueue_prefill_chunk(vx_engine *e, int n, int tok0, int vstart, int 
   }
   (void)hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * DIM, DIM * 4, hipMemcpyDeviceToDevice, st);
   hipLaunchKernelGGL(final_norm_kernel, dim3(1), dim3(1024), 0, st, e->x, e->final_norm,
-                     e->cfg.norm_eps, e->normed, nullptr);
+                     e->cfg.norm_eps, e->normed, nullptr, nullptr);
   hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, st, e->pos, pos0 + n);
   e->host_pos = pos0 + n;
   return VX_OK;
@@ -2271,6 +2286,45 @@ int vx_time_backbone_steps(vx_engine *e, int32_t n, int32_t mode, float *out_ms)
   HIPCHK(e, hipEventSynchronize(e->ev1));
   if (!hold) e->host_pos += n;
   HIPCHK(e, hipEventElapsedTime(out_ms, e->ev0, e->ev1));
+  return VX_OK;
+}
+
+// every slot to (start ~0, end 0): slots of blocks a launch does not have
+// drop out of the host's min / max
+__global__ void timeline_reset_kernel(unsigned long long *ts, size_t slots) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < slots; i += (size_t)gridDim.x * blockDim.x) {
+    ts[2 * i] = ~0ull;
+    ts[2 * i + 1] = 0ull;
+  }
+}
+
+int vx_debug_timeline(vx_engine *e, int32_t reps, uint64_t *stamps, int32_t cap, int32_t *n_out) {
+  if (!e || reps < 1 || !stamps || !n_out) return e ? fail(e, VX_E_INVALID, "bad timeline arguments") : VX_E_INVALID;
+  int rc = check_ready(e);
+  if (rc) return rc;
+  const int n = 6 * e->cfg.n_layers + 1;
+  *n_out = n;
+  if (cap < 2 * n) return fail(e, VX_E_RANGE, "timeline: %d stamps, room for %d", 2 * n, cap);
+  if (e->host_pos >= e->max_seq)
+    return fail(e, VX_E_RANGE, "position %d reaches max_seq_len %d", e->host_pos, e->max_seq);
+  const size_t slots = (size_t)n * TS_BLOCKS;
+  for (int r = 0; r < reps; r++) {
+    hipLaunchKernelGGL(timeline_reset_kernel, dim3(256), dim3(256), 0, e->st, e->timeline, slots);
+    LAUNCHCHK(e);
+    if ((rc = run_seq(e, &e->timeline_exec, enqueue_backbone_timeline))) return rc;
+  }
+  std::vector<uint64_t> all(2 * slots);
+  HIPCHK(e, hipMemcpyAsync(all.data(), e->timeline, slots * 16, hipMemcpyDeviceToHost, e->st));
+  HIPCHK(e, hipStreamSynchronize(e->st));
+  for (int i = 0; i < n; i++) {
+    uint64_t s0 = ~0ull, s1 = 0;
+    for (int b = 0; b < TS_BLOCKS; b++) {
+      s0 = std::min(s0, all[((size_t)i * TS_BLOCKS + b) * 2]);
+      s1 = std::max(s1, all[((size_t)i * TS_BLOCKS + b) * 2 + 1]);
+    }
+    stamps[2 * i] = s0;
+    stamps[2 * i + 1] = s1;
+  }
   return VX_OK;
 }
 

@@ -168,6 +168,21 @@ enum Epi : int {
   EPI_QKV = 4,     // FM: q -> out, k -> out_k, v -> out_v (no rope)
 };
 
+// Launch timeline (vx_debug_timeline): block b of a launch writes its start
+// and end time on the 100 MHz wall clock to ts[2 b], ts[2 b + 1] with plain
+// vector stores (distinct addresses: no contention); the host takes the
+// earliest start and the latest end.  ts is null outside that measurement.
+constexpr int TS_BLOCKS = 1024;  // slots per launch (the widest grid is 768 blocks)
+__device__ __forceinline__ void ts_begin(unsigned long long *ts) {
+  if (ts && threadIdx.x == 0) ts[2 * blockIdx.x] = wall_clock64();
+}
+__device__ __forceinline__ void ts_end(unsigned long long *ts) {
+  if (ts) {
+    __syncthreads();
+    if (threadIdx.x == 0) ts[2 * blockIdx.x + 1] = wall_clock64();
+  }
+}
+
 struct GemvArgs {
   const uint16_t *W;   // [M][K]
   const uint16_t *W2;  // SwiGLU up matrix [M][K]
@@ -185,6 +200,7 @@ struct GemvArgs {
   int kv_f32;     // 1: f32 cache elements (the reference's), 0: f16
   int max_seq;
   const float *inv_freq;  // rope: 1 / theta^(2i/HD), i < HD/2
+  unsigned long long *ts;  // launch timeline slot (passed as gemv1_kernel's ts argument), or null
 };
 
 // one K/V cache element pair (d, d+1) of head row `row` at position pos
@@ -425,7 +441,9 @@ __device__ __forceinline__ void unit_epilogue(const GemvArgs &a, int unit, const
 
 template <int WAVES, int UPW, int UPG, int EPI, bool NORM, int K, int D>
 __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(const uint16_t *W, const uint16_t *W2, const float *x,
-                                                          const uint16_t *norm_w, float *out, GemvArgs args) {
+                                                          const uint16_t *norm_w, float *out,
+                                                          unsigned long long *ts, GemvArgs args) {
+  ts_begin(ts);
   // the pointers the first loads need arrive as leading scalar arguments,
   // which the hardware preloads into SGPRs at wave launch (no kernel-
   // argument load before the first weight load)
@@ -525,6 +543,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(const uint16_t *W, co
         unit_epilogue<EPI>(a, u0 + g * UPG + u, acc + u * RU, pos, resid[g * UPG + u]);
     }
   }
+  ts_end(ts);
 }
 
 // ------------------------------------------------------ decode attention
@@ -536,6 +555,7 @@ struct AttnArgs {
   int max_seq;
   float *part;      // [NH][ATTN_SPLITS][HD + 2] (o, m, l)
   float *out;       // [NH*HD]
+  unsigned long long *ts;  // launch timeline slot (passed as the kernel's ts argument), or null
 };
 
 constexpr int AT_T = 32;  // keys per LDS tile
@@ -598,7 +618,9 @@ __device__ __forceinline__ float2 vpair(const uint16_t *v) {
 // while the current one is computed.
 template <typename KVT>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const void *kc, const void *vc,
-                                                           const float *q, AttnArgs args) {
+                                                           const float *q, unsigned long long *ts,
+                                                           AttnArgs args) {
+  ts_begin(ts);
   // the position, cache and query pointers arrive preloaded in SGPRs: the
   // position load, and the tile loads behind it, wait on no argument load
   AttnArgs a = args;
@@ -672,6 +694,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const
     pp[HD] = m;
     pp[HD + 1] = l;
   }
+  ts_end(ts);
 }
 
 // Combine: one wave per query head; block b combines query head
@@ -680,7 +703,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const
 // M) / L (splits without keys carry m = -inf, l = 0).  Every load of the head
 // (m, l of each split, both output dims of each split) is issued before the
 // first is used: one memory round trip.
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, float *out) {
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, float *out,
+                                                          unsigned long long *ts) {
+  ts_begin(ts);
   const int h = (NH / NKV) * ((int)blockIdx.x % NKV) + (int)blockIdx.x / NKV;
   const int lane = threadIdx.x;
   static_assert(ATTN_SPLITS <= 64, "one lane per split");
@@ -705,6 +730,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, flo
   }
   out[h * HD + lane * 2] = r0 / L;
   out[h * HD + lane * 2 + 1] = r1 / L;
+  ts_end(ts);
 }
 
 // ------------------------------------------------------- small kernels
@@ -751,7 +777,9 @@ __global__ void multi_codebook_kernel(const uint16_t *table, const uint32_t *sem
 // Final rmsNorm into `normed`; also advances the device decode position
 // after every kernel of the step has read it.
 __global__ __launch_bounds__(1024) void final_norm_kernel(const float *x, const uint16_t *w,
-                                                          float eps, float *normed, int *pos) {
+                                                          float eps, float *normed, int *pos,
+                                                          unsigned long long *ts) {
+  ts_begin(ts);
   __shared__ float red[16];
   const int tid = threadIdx.x;
   static_assert(DIM % 1024 == 0, "threads tile DIM");
@@ -774,6 +802,7 @@ __global__ __launch_bounds__(1024) void final_norm_kernel(const float *x, const 
 #pragma unroll
   for (int j = 0; j < DIM / 1024; j++) normed[tid + j * 1024] = xv[j] * rms * gv[j];
   if (pos != nullptr && tid == 0) *pos += 1;
+  ts_end(ts);
 }
 
 // argmax with the reference's 256-lane strided scan and tree (strict '>').

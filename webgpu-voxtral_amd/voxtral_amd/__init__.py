@@ -122,6 +122,7 @@ _SIGS = {
     "vx_time_frames": (_I32, [_VP, _I32, ctypes.POINTER(ctypes.c_float)]),
     "vx_time_kernel": (_I32, [_VP, _I32, _I32, ctypes.POINTER(ctypes.c_float),
                               ctypes.POINTER(ctypes.c_double)]),
+    "vx_debug_timeline": (_I32, [_VP, _I32, _VP, _I32, ctypes.POINTER(_I32)]),
     "vx_synchronize": (_I32, [_VP]),
 }
 
@@ -521,6 +522,18 @@ class VoxtralEngine:
         self._check(self._lib.vx_time_kernel(self._h, int(kernel), int(iters), ctypes.byref(us),
                                              ctypes.byref(b)))
         return us.value, b.value
+
+    def timeline(self, reps=2):
+        """Launch timeline of one held decode step (vx_debug_timeline): an
+        [n][2] array of (earliest block start, latest block end) per launch on
+        the GPU's 100 MHz wall clock, launch 6 l + k of layer l (k: QKV,
+        attention partials, combine, O, gate/up, down), then the final norm."""
+        n = 6 * self.config.n_layers + 1
+        out = np.zeros(2 * n, np.uint64)
+        got = ctypes.c_int32()
+        self._check(self._lib.vx_debug_timeline(self._h, int(reps), out.ctypes.data, out.size,
+                                                ctypes.byref(got)))
+        return out.reshape(got.value, 2)
 
     def synchronize(self):
         self._check(self._lib.vx_synchronize(self._h))
