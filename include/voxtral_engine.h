@@ -109,6 +109,25 @@ int vx_read_tensor(vx_engine *e, const char *name, uint16_t *f16, size_t numel);
 int vx_load_safetensors(vx_engine *e, const char *path, int32_t *n_loaded,
                         int32_t *n_skipped);
 
+/* Per-tensor progress of a weight load, the fields of HFLoadProgress /
+ * WeightLoadProgress (src/weights.ts:149-154, 465-472): `loaded` of `total`
+ * tensors the engine takes from the file, the tensor's component
+ * (classifyComponent, src/weights.ts:478-483: backbone, fm, codec) and name,
+ * and the bytes read from the file so far. */
+typedef void (*vx_load_cb)(void *user, int32_t loaded, int32_t total,
+                           const char *component, const char *tensor,
+                           uint64_t bytes_read);
+/* vx_load_safetensors with on_tensor (nullable) called after each tensor is
+ * on the device, tensors in component order backbone, fm, codec as
+ * loadWeightsFromHF orders them (src/weights.ts:520-523). */
+int vx_load_safetensors_progress(vx_engine *e, const char *path,
+                                 vx_load_cb on_tensor, void *user,
+                                 int32_t *n_loaded, int32_t *n_skipped);
+/* organizeWeights' "Missing weight: <name>" check (src/engine.ts:663-667):
+ * 1 and the first weight not yet loaded (name truncated to cap bytes with a
+ * terminating NUL), or 0 when every weight is loaded. */
+int vx_missing_tensor(const vx_engine *e, char *name, int32_t cap);
+
 /* The two conversions above, on the host (no device needed). */
 void vx_bf16_to_f16(const uint16_t *bf16, uint16_t *f16, size_t n);
 void vx_f32_to_f16_trunc(const float *f32, uint16_t *f16, size_t n);

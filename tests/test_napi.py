@@ -39,7 +39,7 @@ e.init().then(() => console.log(JSON.stringify({{names, ready, msg, init: 'ok'}}
     r = json.loads(out.strip().splitlines()[-1])
     assert r["names"] == sorted(["create", "destroy", "loadTensor", "loadSafetensors", "codecDecode",
                                  "tokenizerCreate", "tokenizerEncode",
-                                 "initSynthetic", "isReady",
+                                 "initSynthetic", "isReady", "missingTensor",
                                  "reset", "position", "backboneStep", "backboneLayers", "fmForward",
                                  "setSemanticCode", "read", "generate"])
     assert r["ready"] is False
@@ -164,6 +164,114 @@ const m = require({json.dumps(JS)});
         g.load_tensor("layers.0.ffn_norm.weight", V.bf16_to_f16(to_bf16_bits(fn)), [3072])
         g.load_tensor("norm.weight", V.f32_to_f16_trunc(fn), [3072])
         _, normed = g.backbone_step(24)
+    finally:
+        g.destroy()
+    assert np.array_equal(np.float32(r["normed"]), normed[:8])
+
+
+def write_manifest_dir(d, components):
+    """The reference's pre-extracted F16 format (src/weights.ts:14-32): one
+    .bin per component, manifest.json listing each tensor's file, offset,
+    size, shape, dtype and component.  components: {component: {name: f16}}"""
+    import numpy as np
+    tensors = {}
+    for comp, ts in components.items():
+        blob, off = bytearray(), 0
+        for name, arr in ts.items():
+            b = np.ascontiguousarray(arr, np.float16).tobytes()
+            tensors[name] = {"file": f"{comp}.bin", "offset": off, "size": len(b),
+                             "padded_size": len(b), "shape": list(np.shape(arr)), "dtype": "f16",
+                             "component": comp}
+            blob += b
+            off += len(b)
+        (d / f"{comp}.bin").write_bytes(bytes(blob))
+    (d / "manifest.json").write_text(json.dumps({"format": "f16", "source": "test",
+                                                 "total_tensors": len(tensors), "tensors": tensors}))
+
+
+@pytest.mark.gpu
+def test_load_weights_manifest_and_progress(tmp_path):
+    """loadWeights(baseUrl, onProgress) of the reference's manifest format
+    (src/engine.ts:539-566, src/weights.ts:317-369) with its
+    WeightLoadProgress events, EngineOptions.onWeightProgress / onProgress /
+    weightsUrl (src/engine.ts:213-219), loadWeightsFromHF's HFLoadProgress
+    events (src/weights.ts:465-472, 520-523, 629-636), and organizeWeights'
+    "Missing weight" error (src/engine.ts:663-667)."""
+    import numpy as np
+    from test_gpu_loader import to_bf16_bits, write_safetensors
+    import voxtral_amd as V
+    rng = np.random.default_rng(12)
+    fn = (1 + rng.standard_normal(3072) * 0.1).astype(np.float16)
+    an = (1 + rng.standard_normal(3072) * 0.1).astype(np.float16)
+    mdir = tmp_path / "m"
+    mdir.mkdir()
+    write_manifest_dir(mdir, {
+        "backbone": {"layers.0.ffn_norm.weight": fn, "norm.weight": an},
+        "fm": {"acoustic_transformer.norm.weight": an},
+        "codec": {"audio_tokenizer.decoder.x": np.zeros(4, np.float16)}})
+    st = tmp_path / "w.safetensors"
+    sn = (1 + rng.standard_normal(3072) * 0.1).astype(np.float32)
+    write_safetensors(st, {"layers.0.attention_norm.weight": ("BF16", to_bf16_bits(sn)),
+                           "acoustic_transformer.layers.0.ffn_norm.weight": ("F32", sn),
+                           "audio_tokenizer.y": ("F32", np.zeros(2, np.float32)),
+                           "norm.weight": ("F16", an)})
+    script = f"""
+const m = require({json.dumps(JS)});
+(async () => {{
+  const msgs = [], wev = [], hev = [];
+  const e = new m.VoxtralEngine({{config: {{backbone: {{n_layers: 1}}, codec: false}}, maxSeqLen: 16,
+    weightsUrl: {json.dumps(str(mdir))}, onProgress: (s) => msgs.push(s), onWeightProgress: (p) => wev.push(p)}});
+  await e.init();
+  e.initSynthetic(0, 0.02);
+  const r = await e.loadWeights();
+  const r2 = await e.loadWeightsFromHF({json.dumps(str(st))}, (p) => hev.push(p));
+  const normed = await e.debugBackboneStepFull(24);
+  e.destroy();
+  const f = new m.VoxtralEngine({{config: {{backbone: {{n_layers: 1}}, codec: false}}, maxSeqLen: 16}});
+  await f.init();
+  let missing = '';
+  try {{ await f.loadWeights({json.dumps(str(mdir))}); }} catch (x) {{ missing = x.message; }}
+  f.destroy();
+  console.log(JSON.stringify({{r, r2, msgs, wev, hev, missing, normed: Array.from(normed.slice(0, 8))}}));
+}})().catch((err) => {{ console.error(err); process.exit(3); }});
+"""
+    print("[napi] loadWeights: manifest + progress", flush=True)
+    r = json.loads(run_node(script, timeout=300).strip().splitlines()[-1])
+    assert r["r"] == {"loaded": 3, "skipped": 1}
+    assert r["r2"] == {"loaded": 3, "skipped": 1}
+    w = r["wev"]
+    assert w[0] == {"loaded": 0, "total": 3, "component": "all", "tensor": "Loading backbone..."}
+    assert w[1] == {"loaded": 0, "total": 2, "component": "backbone", "tensor": "downloading backbone.bin..."}
+    assert w[2] == {"loaded": 1, "total": 2, "component": "backbone", "tensor": "layers.0.ffn_norm.weight"}
+    assert w[3] == {"loaded": 2, "total": 2, "component": "backbone", "tensor": "norm.weight"}
+    assert w[4]["tensor"] == "Loading FM transformer..." and w[-1] == {
+        "loaded": 3, "total": 3, "component": "all", "tensor": "Done!"}
+    h = r["hev"]
+    assert h[0]["component"] == "init" and h[0]["loaded"] == 0 and h[0]["total"] == 3
+    # one event per tensor, component order backbone, fm (codec skipped: no decoder)
+    assert [(x["loaded"], x["component"], x["tensor"]) for x in h[1:]] == [
+        (1, "backbone", "layers.0.attention_norm.weight"), (2, "backbone", "norm.weight"),
+        (3, "fm", "acoustic_transformer.layers.0.ffn_norm.weight")]
+    assert all(x["total"] == 3 and x["cached"] is False for x in h)
+    b = [x["bytesDownloaded"] for x in h]
+    assert b == sorted(b) and b[-1] <= st.stat().st_size
+    assert any("Loading weights from" in s for s in r["msgs"])
+    assert r["missing"].startswith("Missing weight: ")
+    g = V.VoxtralEngine(V.default_config(n_layers=1, codec=0), max_seq_len=16).init()
+    try:
+        g.init_synthetic(0, 0.02)
+        g.load_tensor("layers.0.ffn_norm.weight", fn.view(np.uint16), [3072])
+        g.load_tensor("norm.weight", an.view(np.uint16), [3072])
+        g.load_tensor("acoustic_transformer.norm.weight", an.view(np.uint16), [3072])
+        g.load_tensor("layers.0.attention_norm.weight", V.bf16_to_f16(to_bf16_bits(sn)), [3072])
+        g.load_tensor("acoustic_transformer.layers.0.ffn_norm.weight", V.f32_to_f16_trunc(sn), [3072])
+        _, normed = g.backbone_step(24)
+        events = []
+        g.init_synthetic(1, 0.02)
+        assert g.load_safetensors(st, events.append) == (3, 1)
+        assert [e["tensor"] for e in events] == ["layers.0.attention_norm.weight", "norm.weight",
+                                                 "acoustic_transformer.layers.0.ffn_norm.weight"]
+        assert g.missing_tensor() is None
     finally:
         g.destroy()
     assert np.array_equal(np.float32(r["normed"]), normed[:8])

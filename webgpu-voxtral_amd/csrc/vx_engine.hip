@@ -1128,6 +1128,21 @@ void vx_f32_to_f16_trunc(const float *in, uint16_t *out, size_t n) {
 }
 
 int vx_load_safetensors(vx_engine *e, const char *path, int32_t *n_loaded, int32_t *n_skipped) {
+  return vx_load_safetensors_progress(e, path, nullptr, nullptr, n_loaded, n_skipped);
+}
+
+int vx_missing_tensor(const vx_engine *e, char *name, int32_t cap) {
+  if (!e) return 0;
+  for (auto &kv : e->slots)
+    if (!kv.second.loaded) {
+      if (name && cap > 0) snprintf(name, (size_t)cap, "%s", kv.first.c_str());
+      return 1;
+    }
+  return 0;
+}
+
+int vx_load_safetensors_progress(vx_engine *e, const char *path, vx_load_cb on_tensor, void *user,
+                                 int32_t *n_loaded, int32_t *n_skipped) {
   if (!e || !path) return VX_E_INVALID;
   const int fd = open(path, O_RDONLY);
   if (fd < 0) return fail(e, VX_E_INVALID, "cannot open %s", path);
@@ -1169,6 +1184,16 @@ int vx_load_safetensors(vx_engine *e, const char *path, int32_t *n_loaded, int32
     if (t.shape != sl.shape) return fail(e, VX_E_INVALID, "%s: shape mismatch", kv.first.c_str());
     work.push_back({&kv.first, &sl});
   }
+  // component order backbone, fm, codec (src/weights.ts:520-523); names in
+  // order within a component
+  auto rank = [](const std::string &n) {
+    const char *c = st_component(n);
+    return !strcmp(c, "backbone") ? 0 : !strcmp(c, "fm") ? 1 : 2;
+  };
+  std::stable_sort(work.begin(), work.end(),
+                   [&](const auto &a, const auto &b) { return rank(*a.first) < rank(*b.first); });
+  uint64_t bytes_read = 8 + hlen;
+  int32_t done_tensors = 0;
   // stream each tensor through a device staging buffer; convert on the GPU
   constexpr size_t CH = 256u << 20;
   void *stage = nullptr;
@@ -1201,8 +1226,12 @@ int vx_load_safetensors(vx_engine *e, const char *path, int32_t *n_loaded, int32
         HIPCHK(e, hipStreamSynchronize(e->st));
       }
       done += len;
+      bytes_read += len;
     }
     w.second->loaded = true;
+    done_tensors++;
+    if (on_tensor)
+      on_tensor(user, done_tensors, (int32_t)work.size(), st_component(*w.first), w.first->c_str(), bytes_read);
   }
   e->weights_changed();
   if (n_loaded) *n_loaded = (int32_t)work.size();

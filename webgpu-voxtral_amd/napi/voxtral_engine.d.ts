@@ -14,9 +14,36 @@ export interface VoxtralConfig {
   codec?: boolean;
 }
 
+/** src/weights.ts:149-154 */
+export interface WeightLoadProgress {
+  loaded: number;
+  total: number;
+  component: string;
+  tensor: string;
+}
+
+/** src/weights.ts:465-472 */
+export interface HFLoadProgress {
+  loaded: number;
+  total: number;
+  component: string;
+  tensor: string;
+  /** always false here: the weights come from local files */
+  cached: boolean;
+  /** bytes read from the files so far */
+  bytesDownloaded: number;
+}
+
+/** src/engine.ts:213-219 */
 export interface EngineOptions {
   config?: VoxtralConfig;
   maxSeqLen?: number;
+  /** default location of loadWeights / loadWeightsFromHF (a local path) */
+  weightsUrl?: string;
+  /** stage messages (engine creation, weight loading) */
+  onProgress?: (msg: string) => void;
+  /** default per-tensor callback of loadWeights */
+  onWeightProgress?: (progress: WeightLoadProgress) => void;
 }
 
 export interface TTSResult {
@@ -45,9 +72,13 @@ export interface GenerateOptions {
 export declare class VoxtralEngine {
   constructor(options?: EngineOptions);
   init(): Promise<void>;
-  /** a local .safetensors file or a directory of shards in place of the base URL */
-  loadWeights(location: string): Promise<{ loaded: number; skipped: number }>;
-  loadWeightsFromHF(location: string): Promise<{ loaded: number; skipped: number }>;
+  /** a local directory in place of the base URL: manifest.json + .bin files (the
+   *  pre-extracted f16 format), or *.safetensors shards; or one .safetensors file */
+  loadWeights(baseUrl?: string, onProgress?: (progress: WeightLoadProgress) => void):
+    Promise<{ loaded: number; skipped: number }>;
+  /** a local .safetensors file (or directory of shards) in place of the URL */
+  loadWeightsFromHF(safetensorsUrl?: string, onProgress?: (progress: HFLoadProgress) => void):
+    Promise<{ loaded: number; skipped: number }>;
   loadSafetensors(file: string): { loaded: number; skipped: number };
   loadTensor(name: string, f16: Uint16Array, shape: number[]): void;
   initSynthetic(seed?: number, std?: number): void;

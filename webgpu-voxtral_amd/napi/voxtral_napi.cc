@@ -270,15 +270,54 @@ napi_value load_tensor(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
-// loadSafetensors(h, path) -> {loaded, skipped}
+// loadSafetensors(h, path[, onTensor]) -> {loaded, skipped}.  onTensor(loaded,
+// total, component, tensor, bytesRead) is called on this thread after each
+// tensor reaches the device; once it throws, it is not called again and the
+// exception propagates when the load returns.
+struct LoadProgress {
+  napi_env env;
+  napi_value fn;
+  bool failed;
+};
+static void load_progress(void *user, int32_t loaded, int32_t total, const char *component,
+                          const char *tensor, uint64_t bytes) {
+  auto *p = (LoadProgress *)user;
+  if (p->failed) return;
+  napi_value args[5], global, ret;
+  napi_create_int32(p->env, loaded, &args[0]);
+  napi_create_int32(p->env, total, &args[1]);
+  napi_create_string_utf8(p->env, component, NAPI_AUTO_LENGTH, &args[2]);
+  napi_create_string_utf8(p->env, tensor, NAPI_AUTO_LENGTH, &args[3]);
+  napi_create_double(p->env, (double)bytes, &args[4]);
+  napi_get_global(p->env, &global);
+  if (napi_call_function(p->env, global, p->fn, 5, args, &ret) != napi_ok) p->failed = true;
+  bool pending = false;
+  napi_is_exception_pending(p->env, &pending);
+  if (pending) p->failed = true;
+}
+
 napi_value load_safetensors(napi_env env, napi_callback_info info) {
   Args a;
   if (!get_args(env, info, a) || a.n < 2) return nullptr;
   vx_engine *e = handle(env, a.v[0]);
   if (!e) return nullptr;
   std::string path = str(env, a.v[1]);
+  LoadProgress prog{env, nullptr, false};
+  if (a.n > 2 && !is_nullish(env, a.v[2])) {
+    napi_valuetype t;
+    napi_typeof(env, a.v[2], &t);
+    if (t != napi_function) {
+      napi_throw_type_error(env, nullptr, "onTensor must be a function");
+      return nullptr;
+    }
+    prog.fn = a.v[2];
+  }
   int32_t loaded = 0, skipped = 0;
-  int rc = vx_load_safetensors(e, path.c_str(), &loaded, &skipped);
+  int rc = vx_load_safetensors_progress(e, path.c_str(), prog.fn ? load_progress : nullptr, &prog,
+                                        &loaded, &skipped);
+  bool pending = false;
+  napi_is_exception_pending(env, &pending);
+  if (pending) return nullptr;
   if (rc) return throw_vx(env, e, rc);
   napi_value o, x;
   NAPI_OK(env, napi_create_object(env, &o));
@@ -287,6 +326,22 @@ napi_value load_safetensors(napi_env env, napi_callback_info info) {
   NAPI_OK(env, napi_create_int32(env, skipped, &x));
   NAPI_OK(env, napi_set_named_property(env, o, "skipped", x));
   return o;
+}
+
+// missingTensor(h) -> the first weight not loaded yet, or null
+napi_value missing_tensor(napi_env env, napi_callback_info info) {
+  Args a;
+  if (!get_args(env, info, a) || a.n < 1) return nullptr;
+  vx_engine *e = handle(env, a.v[0]);
+  if (!e) return nullptr;
+  char name[512];
+  napi_value r;
+  if (vx_missing_tensor(e, name, (int32_t)sizeof name)) {
+    napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &r);
+  } else {
+    napi_get_null(env, &r);
+  }
+  return r;
 }
 
 // codecDecode(h, Uint32Array semantic, Uint32Array acoustic[, stop]) ->
@@ -854,6 +909,7 @@ napi_value init(napi_env env, napi_value exports) {
              {"tokenizerEncode", tokenizer_encode},
              {"initSynthetic", init_synthetic},
              {"isReady", is_ready},
+             {"missingTensor", missing_tensor},
              {"reset", reset},
              {"position", position},
              {"backboneStep", backbone_step},

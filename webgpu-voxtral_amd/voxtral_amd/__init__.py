@@ -65,6 +65,8 @@ class GenerateStats(ctypes.Structure):
 FRAME_CB = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int32, ctypes.c_uint32,
                             ctypes.POINTER(ctypes.c_uint32))
 STAGE_CB = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int32, ctypes.c_double)
+_LOAD_CB = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_char_p,
+                            ctypes.c_char_p, ctypes.c_uint64)
 
 FRAME_SAMPLES = 1920  # 80 ms of 24 kHz audio per frame (VX_FRAME_SAMPLES)
 NAC = 36
@@ -88,6 +90,8 @@ _SIGS = {
     "vx_is_ready": (_I32, [_VP]),
     "vx_prefill": (_I32, [_VP, _VP, _I32, _I32, _I32, _VP]),
     "vx_load_safetensors": (_I32, [_VP, ctypes.c_char_p, _VP, _VP]),
+    "vx_load_safetensors_progress": (_I32, [_VP, ctypes.c_char_p, _VP, _VP, _VP, _VP]),
+    "vx_missing_tensor": (_I32, [_VP, ctypes.c_char_p, _I32]),
     "vx_bf16_to_f16": (None, [_VP, _VP, ctypes.c_size_t]),
     "vx_f32_to_f16_trunc": (None, [_VP, _VP, ctypes.c_size_t]),
     "vx_sample_top_p": (_I32, [_VP, _VP, _I32, _I32, ctypes.c_double, ctypes.c_double, _VP, _I32,
@@ -261,13 +265,40 @@ class VoxtralEngine:
         self._check(self._lib.vx_read_tensor(self._h, name.encode(), out.ctypes.data, out.size))
         return out
 
-    def load_safetensors(self, path):
+    def load_safetensors(self, path, on_progress=None):
         """loadWeightsFromHF from a local safetensors file; returns
-        (tensors loaded, tensors skipped)."""
+        (tensors loaded, tensors skipped).  on_progress(dict) after each
+        tensor, with HFLoadProgress's fields (src/weights.ts:465-472):
+        loaded, total, component, tensor, cached (False), bytesDownloaded
+        (bytes read from the file)."""
         n, k = ctypes.c_int32(), ctypes.c_int32()
-        self._check(self._lib.vx_load_safetensors(self._h, os.fsencode(path), ctypes.byref(n),
-                                                  ctypes.byref(k)))
+        if on_progress is None:
+            self._check(self._lib.vx_load_safetensors(self._h, os.fsencode(path), ctypes.byref(n),
+                                                      ctypes.byref(k)))
+            return n.value, k.value
+        errors = []
+
+        def cb(_user, loaded, total, component, tensor, nbytes):
+            if errors:
+                return
+            try:
+                on_progress({"loaded": loaded, "total": total, "component": component.decode(),
+                             "tensor": tensor.decode(), "cached": False, "bytesDownloaded": nbytes})
+            except BaseException as e:  # re-raised after the load returns
+                errors.append(e)
+        c_cb = _LOAD_CB(cb)
+        rc = self._lib.vx_load_safetensors_progress(self._h, os.fsencode(path), c_cb, None,
+                                                    ctypes.byref(n), ctypes.byref(k))
+        if errors:
+            raise errors[0]
+        self._check(rc)
         return n.value, k.value
+
+    def missing_tensor(self):
+        """The first weight not loaded yet (organizeWeights' "Missing weight",
+        src/engine.ts:663-667), or None."""
+        buf = ctypes.create_string_buffer(512)
+        return buf.value.decode() if self._lib.vx_missing_tensor(self._h, buf, len(buf)) else None
 
     def init_synthetic(self, seed=0, std=0.02):
         self._check(self._lib.vx_init_synthetic(self._h, seed, std))
