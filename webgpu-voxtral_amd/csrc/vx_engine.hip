@@ -301,11 +301,11 @@ static void enqueue_layer(vx_engine *e, int l, int only = -1, unsigned long long
   if (only < 0 || only == VX_KERNEL_ATTN) {
     AttnArgs a{e->q, e->kc(l), e->vc(l), e->pos, e->max_seq, e->part, e->attn, slot(1)};
     if (e->kv_f32)
-      hipLaunchKernelGGL(attn_partial_kernel<float>, attn_grid(), dim3(256), 0, st, a.pos, a.kc,
-                         a.vc, a.q, a.ts, a);
+      hipLaunchKernelGGL(attn_partial_kernel<float>, attn_grid(), dim3(256), KvRing<float>::LDS, st, a.pos,
+                         a.kc, a.vc, a.q, a.ts, a);
     else
-      hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, attn_grid(), dim3(256), 0, st, a.pos, a.kc,
-                         a.vc, a.q, a.ts, a);
+      hipLaunchKernelGGL(attn_partial_kernel<uint16_t>, attn_grid(), dim3(256), KvRing<uint16_t>::LDS, st,
+                         a.pos, a.kc, a.vc, a.q, a.ts, a);
     hipLaunchKernelGGL(attn_combine_kernel, dim3(NH), dim3(64), 0, st, e->part, e->attn, slot(2));
   }
   if (only < 0 || only == VX_KERNEL_OPROJ) {
@@ -739,6 +739,15 @@ int vx_create(const vx_config *cfg_in, int32_t max_seq, vx_engine **out) {
   if (hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking) != hipSuccess) {
     delete e;
     return fail(nullptr, VX_E_DEVICE, "hipStreamCreate failed");
+  }
+  // the decode attention partials take 35 KB (f16 cache) or 67 KB (f32)
+  // of dynamic LDS for their two tile stages
+  if (hipFuncSetAttribute((const void *)attn_partial_kernel<float>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          KvRing<float>::LDS) != hipSuccess ||
+      hipFuncSetAttribute((const void *)attn_partial_kernel<uint16_t>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          KvRing<uint16_t>::LDS) != hipSuccess) {
+    vx_destroy(e);
+    return fail(nullptr, VX_E_DEVICE, "attention LDS attribute rejected");
   }
   (void)hipEventCreate(&e->ev0);
   (void)hipEventCreate(&e->ev1);

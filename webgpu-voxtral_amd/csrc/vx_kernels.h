@@ -563,29 +563,38 @@ constexpr int AT_T = 32;  // keys per LDS tile
 // keys per split for seq keys
 __device__ __forceinline__ int attn_chunk(int seq) { return (seq + ATTN_SPLITS - 1) / ATTN_SPLITS; }
 
-// Geometry of one K or V tile of AT_T rows staged through LDS: 16-byte
-// chunks, CPT per thread (256 threads), rows padded by 16 bytes so that the
-// 32 lanes reading 32 different K rows at one column spread over the banks.
+// One K or V tile of AT_T key rows in LDS, filled by direct global->LDS
+// loads (global_load_lds_dwordx4: 64 lanes x 16 bytes = one 1 KB block per
+// instruction, no registers, no staging stores).  Chunk c (16 bytes) of tile
+// row r sits at position c ^ kv_sw(r) of its LDS row: the lanes of one score
+// read (keys 0..7 x both halves, see the partial kernel) then hit 16
+// distinct 16-byte bank groups, and a row read for the value product is a
+// permutation of the row.
 template <typename KVT>
-struct KvTile {
-  static constexpr int EPC = 16 / (int)sizeof(KVT);  // elements per chunk
-  static constexpr int CPR = HD / EPC;                // chunks per row
-  static constexpr int CPT = AT_T * CPR / 256;        // chunks per thread
-  static constexpr int LDW = HD + EPC;                // LDS row stride (elements)
+struct KvRing {
+  static constexpr int RB = HD * (int)sizeof(KVT);  // bytes per key row
+  static constexpr int CPR = RB / 16;               // 16-byte chunks per row
+  static constexpr int RPB = 1024 / RB;             // rows per 1 KB load
+  static constexpr int TB = AT_T * RB;              // bytes of one K (or V) tile
+  static constexpr int BPT = TB / 1024;             // 1 KB loads per K tile
+  static constexpr int LPW = BPT / 2;               // loads per wave per tile (K and V)
+  static constexpr int EPC = 16 / (int)sizeof(KVT);
+  static constexpr int STAGES = 2;                  // tile t + 1 loads while tile t is used
+  static constexpr int LDS = 2048 + STAGES * 2 * TB;  // query heads + K|V stages
 };
+__device__ __forceinline__ int kv_sw(int r) { return (2 * r) & 15; }
 
-template <typename KVT>
-__device__ __forceinline__ void attn_load_tile(const KVT *Kb, const KVT *Vb, int pb, int n, int tid,
-                                               u32x4 (&kr)[KvTile<KVT>::CPT],
-                                               u32x4 (&vr)[KvTile<KVT>::CPT]) {
-  using G = KvTile<KVT>;
-#pragma unroll
-  for (int i = 0; i < G::CPT; i++) {
-    const int id = tid + 256 * i, row = id / G::CPR, col = id % G::CPR;
-    const size_t off = (size_t)(pb + min(row, n - 1)) * HD + col * G::EPC;  // rows past n re-read row n-1
-    kr[i] = *(const u32x4 *)(Kb + off);
-    vr[i] = *(const u32x4 *)(Vb + off);
-  }
+__device__ __forceinline__ void lds_dma16(const void *src, unsigned char *lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+// s_waitcnt immediate for vmcnt(vm), the other counters left open
+constexpr int attn_vmcnt(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (15 << 8); }
+// block barrier for LDS only: waits for this wave's LDS reads, not for its
+// direct loads in flight (a __syncthreads fence would drain those too)
+__device__ __forceinline__ void attn_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // sum over 16 bytes of K elements times 16/sizeof(KVT) query values
@@ -599,10 +608,24 @@ __device__ __forceinline__ float kdot(const float *k, const float *q, float acc)
 __device__ __forceinline__ float kdot(const uint16_t *k, const float *q, float acc) {
   return dot8(*(const u32x4 *)k, *(const f32x4 *)q, *(const f32x4 *)(q + 4), acc);
 }
-__device__ __forceinline__ float2 vpair(const float *v) { return *(const float2 *)v; }
+// two consecutive V elements as floats (scalar loads: the compiler pairs
+// them, and keeps them free of a wait on the direct loads still in flight)
+__device__ __forceinline__ float2 vpair(const float *v) { return make_float2(v[0], v[1]); }
 __device__ __forceinline__ float2 vpair(const uint16_t *v) {
   const h2 p = __builtin_bit_cast(h2, *(const uint32_t *)v);
   return make_float2((float)p.x, (float)p.y);
+}
+// maximum over the wave when lanes 2k and 2k+1 hold the same value: three DPP
+// steps leave each row of 16 lanes holding its maximum, then the four rows
+__device__ __forceinline__ float wave_max_pairs(float v) {
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+  const int b = __builtin_bit_cast(int, v);
+  return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+               fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
 }
 
 // Partials (attnScore + softmax + attnValue, src/shaders.ts:306-447, split
@@ -610,84 +633,105 @@ __device__ __forceinline__ float2 vpair(const uint16_t *v) {
 // block b = split * NKV + kv head.  Workgroups are dealt to the 8 XCDs
 // round-robin, so a KV head's splits (and the combine blocks of its query
 // heads) run on one XCD.  Wave w is query head 4*kv_head + w, so the four
-// heads sharing a KV head share every staged tile.  Split s covers keys
+// heads sharing a KV head share every tile.  Split s covers keys
 // [s*chunk, min(seq, (s+1)*chunk)), chunk = ceil(seq / ATTN_SPLITS).
-// Per tile of AT_T keys: lane l scores key l%32 over dims [(l/32)*64, +64)
-// (halves joined by one shuffle), an online softmax update, then lane l
-// accumulates P.V for dims 2l, 2l+1.  The next tile's loads are in flight
-// while the current one is computed.
+// The block's four query vectors (2 KB) and its key tiles reach LDS by
+// direct loads; two tile stages, so tile t + 1 is in flight while tile t is
+// used.  Per tile of AT_T keys: lanes 2k and 2k+1 score key k over the even
+// and odd 16-byte chunks of the row (joined by one DPP step), the online
+// softmax update takes its maximum and sum by DPP steps, then lane l
+// accumulates P.V for dims 2l, 2l+1 with each key's weight read out of its
+// lane.  Launch with KvRing<KVT>::LDS bytes of dynamic LDS.
 template <typename KVT>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const int *pos, const void *kc, const void *vc,
                                                            const float *q, unsigned long long *ts,
                                                            AttnArgs args) {
   ts_begin(ts);
-  // the position, cache and query pointers arrive preloaded in SGPRs: the
-  // position load, and the tile loads behind it, wait on no argument load
-  AttnArgs a = args;
-  a.pos = pos;
-  a.kc = kc;
-  a.vc = vc;
-  a.q = q;
-  using G = KvTile<KVT>;
+  using G = KvRing<KVT>;
+  extern __shared__ __attribute__((aligned(1024))) unsigned char attn_smem[];
+  unsigned char *qs = attn_smem;           // [4][HD] f32
+  unsigned char *ring = attn_smem + 2048;  // G::STAGES x (K tile | V tile)
   const int split = blockIdx.x / NKV, kvh = blockIdx.x % NKV;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h = kvh * (NH / NKV) + wave;
-  const int seq = *a.pos + 1;
+  // the four query heads first in the load queue: every tile wait covers them
+  if (wave < 2) lds_dma16(q + (size_t)kvh * (NH / NKV) * HD + wave * 256 + lane * 4, qs + wave * 1024);
+  const int seq = *pos + 1;
   const int chunk = attn_chunk(seq);
   const int p0 = min(seq, split * chunk), p1 = min(seq, p0 + chunk);
-  __shared__ __attribute__((aligned(16))) float qs[4][HD];
-  __shared__ __attribute__((aligned(16))) KVT ks[AT_T * G::LDW];
-  __shared__ __attribute__((aligned(16))) KVT vs[AT_T * G::LDW];
-  __shared__ float ps[4][AT_T];
-  const float scale = 1.0f / sqrtf((float)HD);
-  const KVT *Kb = (const KVT *)a.kc + (size_t)kvh * a.max_seq * HD;
-  const KVT *Vb = (const KVT *)a.vc + (size_t)kvh * a.max_seq * HD;
+  const KVT *Kb = (const KVT *)kc + (size_t)kvh * args.max_seq * HD;
+  const KVT *Vb = (const KVT *)vc + (size_t)kvh * args.max_seq * HD;
+  const int nt = (p1 - p0 + AT_T - 1) / AT_T;
 
-  u32x4 kr[G::CPT], vr[G::CPT];
-  if (p0 < p1) attn_load_tile<KVT>(Kb, Vb, p0, min(AT_T, p1 - p0), tid, kr, vr);
-  qs[wave][lane * 2] = a.q[h * HD + lane * 2];
-  qs[wave][lane * 2 + 1] = a.q[h * HD + lane * 2 + 1];
-
-  const int key = lane & (AT_T - 1), half = lane >> 5;
-  float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int pb = p0; pb < p1; pb += AT_T) {
-    const int n = min(AT_T, p1 - pb);
-    __syncthreads();  // the previous tile's LDS reads are done
+  // tile t into stage t % STAGES: load i of wave w fills LDS block 4 i + w,
+  // i.e. rows RPB (4 i + w) + lane / CPR, position lane % CPR; rows past the
+  // split's end re-read its last row
+  auto issue = [&](int t) {
+    const int pb = p0 + t * AT_T, n = min(AT_T, p1 - pb);
+    unsigned char *st = ring + (t % G::STAGES) * 2 * G::TB;
 #pragma unroll
-    for (int i = 0; i < G::CPT; i++) {
-      const int id = tid + 256 * i, row = id / G::CPR, col = id % G::CPR;
-      *(u32x4 *)(ks + row * G::LDW + col * G::EPC) = kr[i];
-      *(u32x4 *)(vs + row * G::LDW + col * G::EPC) = vr[i];
+    for (int i = 0; i < G::BPT / 4; i++) {
+      const int b = 4 * i + wave;
+      const int row = b * G::RPB + lane / G::CPR;
+      const int c = (lane % G::CPR) ^ kv_sw(row);
+      const size_t g = (size_t)(pb + min(row, n - 1)) * HD + c * G::EPC;
+      lds_dma16(Kb + g, st + b * 1024);
+      lds_dma16(Vb + g, st + G::TB + b * 1024);
     }
-    if (pb + AT_T < p1) attn_load_tile<KVT>(Kb, Vb, pb + AT_T, min(AT_T, p1 - pb - AT_T), tid, kr, vr);
-    __syncthreads();
-
-    float dot = 0.f;
-    const KVT *kp = ks + key * G::LDW + half * (HD / 2);
-    const float *qp = &qs[wave][half * (HD / 2)];
+  };
 #pragma unroll
-    for (int c = 0; c < HD / 2; c += G::EPC) dot = kdot(kp + c, qp + c, dot);
-    dot += __shfl_xor(dot, 32, 64);
+  for (int t = 0; t < G::STAGES; t++)
+    if (t < nt) issue(t);
+
+  const float scale = 1.0f / sqrtf((float)HD);
+  const int key = lane >> 1, half = lane & 1;
+  const float *qh = (const float *)qs + wave * HD;
+  float m = -INFINITY, l = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int t = 0; t < nt; t++) {
+    const int n = min(AT_T, p1 - p0 - t * AT_T);
+    // this wave's loads of tile t are in (a later tile's may still fly),
+    // then every wave's
+    if (t + 1 < nt) __builtin_amdgcn_s_waitcnt(attn_vmcnt(G::LPW));
+    else __builtin_amdgcn_s_waitcnt(attn_vmcnt(0));
+    attn_barrier();
+    const unsigned char *Kt = ring + (t % G::STAGES) * 2 * G::TB, *Vt = Kt + G::TB;
+    const unsigned char *kr = Kt + key * G::RB;
+    const int sw = kv_sw(key);
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < G::CPR / 2; i += 2) {
+      const int c0 = 2 * i + half, c1 = c0 + 2;
+      d0 = kdot((const KVT *)(kr + ((c0 ^ sw) << 4)), qh + c0 * G::EPC, d0);
+      d1 = kdot((const KVT *)(kr + ((c1 ^ sw) << 4)), qh + c1 * G::EPC, d1);
+    }
+    float dot = d0 + d1;
+    dot += dpp_mov<0xB1>(dot);  // quad_perm [1,0,3,2]: the pair's other half
     const bool valid = key < n;
     const float s = valid ? dot * scale : -INFINITY;
-    const float mnew = fmaxf(m, wave_max(s));
+    const float mnew = fmaxf(m, wave_max_pairs(s));
     const float e = valid ? expf(s - mnew) : 0.f;
     const float corr = expf(m - mnew);
-    l = l * corr + wave_sum(half ? 0.f : e);
+    l = l * corr + wave_sum_dpp(half ? 0.f : e);
     o0 *= corr;
     o1 *= corr;
     m = mnew;
-    if (!half) ps[wave][key] = e;
-    __syncthreads();
-#pragma unroll 8
+    const int eb = __builtin_bit_cast(int, e);
+#pragma unroll
     for (int j = 0; j < AT_T; j++) {
-      const float ej = ps[wave][j];  // 0 for j >= n
-      const float2 v = vpair(vs + j * G::LDW + lane * 2);
+      const float ej = __builtin_bit_cast(float, __builtin_amdgcn_readlane(eb, 2 * j));  // 0 for j >= n
+      const unsigned char *vr = Vt + j * G::RB;
+      const int vc0 = sizeof(KVT) == 4 ? lane >> 1 : lane >> 2;
+      const int vb = sizeof(KVT) == 4 ? (lane & 1) * 8 : (lane & 3) * 4;
+      const float2 v = vpair((const KVT *)(vr + ((vc0 ^ kv_sw(j)) << 4) + vb));
       o0 = fmaf(ej, v.x, o0);
       o1 = fmaf(ej, v.y, o1);
     }
+    if (t + G::STAGES < nt) {
+      attn_barrier();  // every wave is done with this stage
+      issue(t + G::STAGES);
+    }
   }
-  float *pp = a.part + ((size_t)h * ATTN_SPLITS + split) * (HD + 2);
+  float *pp = args.part + ((size_t)h * ATTN_SPLITS + split) * (HD + 2);
   pp[lane * 2] = o0;
   pp[lane * 2 + 1] = o1;
   if (lane == 0) {
