@@ -74,6 +74,18 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
          (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
           __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
 }
+// maximum over the wave by the same DPP steps as wave_sum_dpp
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+  const int b = __builtin_bit_cast(int, v);
+  return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+               fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
@@ -496,7 +508,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(const uint16_t *W, co
     for (int i = 0; i < XPT; i++)
       if (XEXACT || (tid + i * NT) * 4 < K)
         s += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
-    s = wave_sum(s);
+    s = wave_sum_dpp(s);
     if (lane == 0) red[wave] = s;
     __syncthreads();
     float tot = 0.f;
@@ -536,7 +548,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv1_kernel(const uint16_t *W, co
     }
     if (g + DD < G) load_group<EPI, K, UPG>(a, u0 + (g + DD) * UPG, lane, wbuf[g % DD]);
 #pragma unroll
-    for (int r = 0; r < RG; r++) acc[r] = wave_sum(acc[r]);
+    for (int r = 0; r < RG; r++) acc[r] = wave_sum_dpp(acc[r]);
     if (lane == 0) {
 #pragma unroll
       for (int u = 0; u < UPG; u++)
@@ -762,9 +774,9 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *part, flo
   for (int s = 0; s < ATTN_SPLITS; s++) o[s] = *(const float2 *)(hp + s * (HD + 2) + lane * 2);
   // keep every load ahead of the first use (one memory round trip)
   __builtin_amdgcn_sched_barrier(0);
-  const float M = wave_max(mv);
+  const float M = wave_max_dpp(mv);
   const float wgt = lane_live ? expf(mv - M) : 0.f;
-  const float L = wave_sum(lane_live ? lv * wgt : 0.f);
+  const float L = wave_sum_dpp(lane_live ? lv * wgt : 0.f);
   float r0 = 0.f, r1 = 0.f;
 #pragma unroll
   for (int s = 0; s < ATTN_SPLITS; s++) {
