@@ -292,7 +292,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint16_t *W, con
       for (int i = 0; i < XPV; i++)
         s += xv[b][i].x * xv[b][i].x + xv[b][i].y * xv[b][i].y + xv[b][i].z * xv[b][i].z +
              xv[b][i].w * xv[b][i].w;
-      s = wave_sum(s);
+      s = wave_sum_dpp(s);
       if (lane == 0) red[wave][b] = s;
     }
     __syncthreads();
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const uint16_t *W, con
 #pragma unroll
   for (int r = 0; r < RPW; r++)
 #pragma unroll
-    for (int b = 0; b < NB; b++) acc[r][b] = wave_sum(acc[r][b]);
+    for (int b = 0; b < NB; b++) acc[r][b] = wave_sum_dpp(acc[r][b]);
   if (lane != 0) return;
 
   if (EPI == EPI_SWIGLU) {
@@ -848,7 +848,7 @@ __global__ __launch_bounds__(1024) void final_norm_kernel(const float *x, const 
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < DIM / 1024; j++) s += xv[j] * xv[j];
-  s = wave_sum(s);
+  s = wave_sum_dpp(s);
   if ((tid & 63) == 0) red[tid >> 6] = s;
   __syncthreads();
   float tot = 0.f;
@@ -1200,7 +1200,7 @@ __global__ __launch_bounds__(RG * KS * 64) void gemm6_kernel(const uint16_t *W, 
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; j++) s += lane * 4 + j < a.nssq ? sv[v][j] : 0.f;
-      rs[v] = 1.0f / sqrtf(wave_sum(s) / (float)DIM + a.eps);
+      rs[v] = 1.0f / sqrtf(wave_sum_dpp(s) / (float)DIM + a.eps);
     }
   }
   f32x4 acc[TL];
@@ -1662,7 +1662,7 @@ __global__ __launch_bounds__(256) void fm_step_in_kernel(const uint16_t *w_in, c
   for (int v = 0; v < FMV; v++) {
     a.seq[v * DIM + row] = y[v];
     bpack_put(a.Bn, v, row, y[v] * g);
-    const float s2 = wave_sum(y[v] * y[v]);
+    const float s2 = wave_sum_dpp(y[v] * y[v]);
     if ((t & 63) == 0) red[t >> 6][v] = s2;
   }
   __syncthreads();
@@ -1692,7 +1692,7 @@ __global__ __launch_bounds__(64) void fm_attn_kernel(const float *q, const float
   for (int i = 0; i < 3; i++) {
     float s[3];
 #pragma unroll
-    for (int j = 0; j < 3; j++) s[j] = wave_sum(qv[i][0] * kv[j][0] + qv[i][1] * kv[j][1]) * scale;
+    for (int j = 0; j < 3; j++) s[j] = wave_sum_dpp(qv[i][0] * kv[j][0] + qv[i][1] * kv[j][1]) * scale;
     float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
     float e0 = expf(s[0] - mx), e1 = expf(s[1] - mx), e2 = expf(s[2] - mx);
     float sum = e0 + e1 + e2;
