@@ -1,7 +1,8 @@
 """Engine lifecycle on the device: an engine that has run every captured
 path (decode step graph, frame graphs in both sampling modes with their
 pinned code slots, the codec decoder) gives back all of its device memory
-when destroyed, so a process can create and destroy engines repeatedly."""
+when destroyed, so a process can create and destroy engines repeatedly; and
+a second call or a second engine reproduces generate() bit for bit."""
 import ctypes
 
 import numpy as np
@@ -52,3 +53,27 @@ def test_create_destroy_returns_device_memory():
     # engine kept would show four times over
     assert min(sizes) > 2**30
     assert free_out >= free0 - 256 * 2**20
+
+
+def test_generate_is_bit_identical_across_calls_and_engines():
+    """The same prompt, voice rows and seed give bit-identical codes and
+    audio on a second call and on a second engine (every reduction adds in a
+    fixed order; no float atomics)."""
+    from vxtest import tts_prompt, voice_rows
+    toks, a0, na = tts_prompt(40, 8, seed=4)
+    voice = voice_rows(8)
+    runs = {}
+    for k in range(2):
+        g = gpu_engine(n_layers=2, max_seq=512)
+        for mode in ("greedy", "top_p"):
+            for call in range(2):
+                out = g.generate(toks, a0, na, voice, 10, sampling=mode, seed=7, ignore_eos=True)
+                runs.setdefault(mode, []).append(out)
+        g.destroy()
+    for mode, outs in runs.items():
+        ref = outs[0]
+        for o in outs[1:]:
+            assert o["semanticCodes"] == ref["semanticCodes"], mode
+            assert o["acousticCodes"] == ref["acousticCodes"], mode
+            assert np.array_equal(np.asarray(o["audio"]).view(np.uint32),
+                                  np.asarray(ref["audio"]).view(np.uint32)), mode
