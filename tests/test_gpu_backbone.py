@@ -412,6 +412,32 @@ def test_long_context_decode(kv_f16):
         o.close()
 
 
+def test_long_context_decode_26_layers_f32_kv():
+    """The bench's long-context workload with the reference's f32 KV cache:
+    the full 26-layer backbone decoding consecutive positions 3896..3899
+    over a synthetic N(0,1) cache (122 keys per attention split, four LDS
+    tiles per block).  Hidden states to the 1e-2 bar at every step."""
+    print("[long] 26-layer engines, f32 KV, positions 3896..3899", flush=True)
+    g = gpu_engine(n_layers=26, max_seq=4096)
+    o = oracle_engine(n_layers=26, max_seq=4096)
+    try:
+        g.fill_kv_synthetic(SEED, 3896)
+        fill_oracle_kv(o, SEED, 3896)
+        g.position = 3896
+        o.position = 3896
+        for i in range(4):
+            x = O.gen_f32(SEED + 70 + i, "input.hidden", 3072)
+            _, gn = g.backbone_step(precomputed=x)
+            o.backbone_step(precomputed=x)
+            err = max_rel_err(gn, o.buffer("normed"))
+            print(f"[long] position {3896 + i}: normed max rel err {err:.2e}", flush=True)
+            assert err < 1e-2 and ref_allclose(gn, o.buffer("normed")), (i, err)
+        assert g.position == o.position == 3900
+    finally:
+        g.destroy()
+        o.close()
+
+
 def test_long_context_decode_26_layers_f16_kv():
     """The long-context stress as specified: the full 26-layer backbone with
     the f16 KV cache, decoding consecutive positions 3896..3899 over a
