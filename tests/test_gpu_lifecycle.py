@@ -55,21 +55,25 @@ def test_create_destroy_returns_device_memory():
     assert free_out >= free0 - 256 * 2**20
 
 
-def test_generate_is_bit_identical_across_calls_and_engines():
+@pytest.mark.parametrize("layers,frames", [(2, 10), (26, 200)])
+def test_generate_is_bit_identical_across_calls_and_engines(layers, frames):
     """The same prompt, voice rows and seed give bit-identical codes and
     audio on a second call and on a second engine (every reduction adds in a
-    fixed order; no float atomics)."""
+    fixed order; no float atomics), up to the full 26 layers and 200 frames
+    of the frame-loop workload."""
     from vxtest import tts_prompt, voice_rows
     toks, a0, na = tts_prompt(40, 8, seed=4)
     voice = voice_rows(8)
     runs = {}
     for k in range(2):
-        g = gpu_engine(n_layers=2, max_seq=512)
+        g = gpu_engine(n_layers=layers, max_seq=512)
         for mode in ("greedy", "top_p"):
             for call in range(2):
-                out = g.generate(toks, a0, na, voice, 10, sampling=mode, seed=7, ignore_eos=True)
+                out = g.generate(toks, a0, na, voice, frames, sampling=mode, seed=7, ignore_eos=True)
+                assert out["stats"]["framesGenerated"] == frames
                 runs.setdefault(mode, []).append(out)
         g.destroy()
+        print(f"[determinism] {layers} layers, engine {k}: {frames} frames per call", flush=True)
     for mode, outs in runs.items():
         ref = outs[0]
         for o in outs[1:]:
